@@ -1,0 +1,280 @@
+"""CPU oracle of the Vortex sparse-attention indexer + cache path.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker for the gfx950 kernels:
+only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import it.  The product path (vortex_torch) never calls it and has no CPU
+fallback.
+
+Each function restates one reference function in numpy, following the cited
+reference file:line.  Conventions:
+
+* bf16 data is carried as its raw bit pattern (``np.uint16``);
+* integer division and remainder follow C (truncation toward zero), as the
+  reference's CUDA and Triton code do;
+* floating-point reductions accumulate in float64 and round once to fp32 and
+  then to bf16 (round-to-nearest-even) — the reference GPU code accumulates
+  in bf16 (CMean) or rounds every product to bf16 (GeMV); the north-star
+  contract compares against fp32 accumulation within rtol 1e-2 / atol 1e-3.
+
+How each function is pinned (tests/test_oracle.py): the planner and top-k by
+independent pure-Python restatements on small inputs plus closed-form
+invariants; bf16 rounding against torch's own conversion; the reductions and
+GeMV against torch.amax/amin/mean/matmul in float64 and closed forms.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# --------------------------------------------------------------------------
+# bf16 bit helpers
+# --------------------------------------------------------------------------
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    """bf16 bit patterns -> float32 (exact)."""
+    b = np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)
+    return b.view(np.float32)
+
+
+def f32_to_bf16(x) -> np.ndarray:
+    """float32 -> bf16 bit patterns, round to nearest even; every NaN becomes
+    the quiet NaN 0x7FC0 (as torch's conversion does)."""
+    f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    r = np.where(nan, 0x7FC0, r)
+    return r.astype(np.uint16)
+
+
+def c_div(a, b):
+    """C integer division (truncates toward zero)."""
+    a = np.asarray(a, dtype=np.int64)
+    q = np.abs(a) // abs(int(b))
+    return np.where((a < 0) != (int(b) < 0), -q, q)
+
+
+def c_mod(a, b):
+    """C remainder (sign of the dividend)."""
+    a = np.asarray(a, dtype=np.int64)
+    return a - c_div(a, b) * int(b)
+
+
+def _int16(v: int) -> int:
+    return ((int(v) + 32768) % 65536) - 32768
+
+
+# --------------------------------------------------------------------------
+# A.1 decode planner — csrc/utils_sglang.cu:123-309 (host 313-460)
+# --------------------------------------------------------------------------
+
+
+def plan_decode(seq_lens, req_to_token, req_indices, page_size: int, num_kv_heads: int,
+                topk_val: int, bos: int, eos: int, max_chunk_size: int) -> dict:
+    """Returns the block tables and workload list the reference planner writes.
+
+    Keys: dense_indptr, dense_indices, sparse_indptr, sparse_indices,
+    sparse_written (bool mask: the planner leaves the top-k slots of long
+    segments untouched), kv_last_page_len, winfo_q, winfo_off, winfo_len,
+    num_workloads, chunk_size.
+    """
+    L = np.asarray(seq_lens, dtype=np.int64)
+    r2t = np.asarray(req_to_token, dtype=np.int64)
+    ridx = np.asarray(req_indices, dtype=np.int64)
+    P, H = int(page_size), int(num_kv_heads)
+    B = L.shape[0]
+    budget = topk_val + bos + eos
+    n = c_div(L + P - 1, P)                       # utils_sglang.cu:267
+    sn = np.minimum(budget, n)                    # utils_sglang.cu:282
+
+    # indptr: inclusive pair scan, H entries per request (utils_sglang.cu:257-309)
+    dense_len = np.repeat(n, H)
+    sparse_len = np.repeat(sn, H)
+    dense_indptr = np.zeros(B * H + 1, dtype=np.int64)
+    sparse_indptr = np.zeros(B * H + 1, dtype=np.int64)
+    dense_indptr[1:] = np.cumsum(dense_len)
+    sparse_indptr[1:] = np.cumsum(sparse_len)
+
+    total_dense = int(dense_indptr[-1])
+    total_sparse = int(sparse_indptr[-1])
+    dense = np.zeros(total_dense, dtype=np.int64)
+    sparse = np.zeros(total_sparse, dtype=np.int64)
+    written = np.zeros(total_sparse, dtype=bool)
+    last = np.zeros(B * H, dtype=np.int64)
+
+    # indices (utils_sglang.cu:123-184)
+    for b in range(B):
+        nb = int(n[b])
+        rem = int(c_mod(L[b], P))
+        cols = np.arange(nb, dtype=np.int64) * P
+        phys = c_div(r2t[ridx[b], cols], P) if nb > 0 else np.zeros(0, dtype=np.int64)
+        for h in range(H):
+            s = b * H + h
+            last[s] = P if rem == 0 else rem
+            enc = phys * H + h
+            d0 = int(dense_indptr[s])
+            dense[d0:d0 + nb] = enc
+            s0 = int(sparse_indptr[s])
+            if nb <= budget:
+                sparse[s0:s0 + nb] = enc
+                written[s0:s0 + nb] = True
+            else:
+                sparse[s0:s0 + bos] = enc[:bos]
+                written[s0:s0 + bos] = True
+                for e in range(eos):                   # utils_sglang.cu:174-181
+                    sparse[s0 + budget - 1 - e] = enc[nb - 1 - e]
+                    written[s0 + budget - 1 - e] = True
+
+    # workload list (utils_sglang.cu:188-254): segments in order, chunks of C
+    C = int(max_chunk_size)
+    wq, wo, wl = [], [], []
+    for s in range(B * H):
+        w = _int16(int(dense_indptr[s + 1] - dense_indptr[s]) - bos - eos)
+        pc = (w & 0xFFFF) if w > topk_val else 0
+        nchunks = (pc + C - 1) // C
+        tail = pc % C or C
+        for k in range(nchunks):
+            wq.append(s)
+            wl.append(C if k != nchunks - 1 else tail)
+            wo.append(int(dense_indptr[s]) + k * C + bos)
+
+    return {
+        "dense_indptr": dense_indptr.astype(np.int32),
+        "dense_indices": dense.astype(np.int32),
+        "sparse_indptr": sparse_indptr.astype(np.int32),
+        "sparse_indices": sparse.astype(np.int32),
+        "sparse_written": written,
+        "kv_last_page_len": last.astype(np.int32),
+        "winfo_q": np.asarray(wq, dtype=np.int32),
+        "winfo_off": np.asarray(wo, dtype=np.int32),
+        "winfo_len": np.asarray(wl, dtype=np.int32),
+        "num_workloads": len(wq),
+        "chunk_size": C,
+    }
+
+
+# --------------------------------------------------------------------------
+# A.2 page-finish reduction — cache/triton_kernels/reduce_impl.py:7-62
+# --------------------------------------------------------------------------
+
+MEAN, MAX, MIN, L2NORM = 0, 1, 2, 3
+
+
+def page_reduce(x_bits, out, loc, num_kv_heads: int, page_size: int, dim: int, reduce_type: int):
+    """Returns (new_out, written_rows).
+
+    x_bits: uint16 [rows, R, C] (bf16 bits).  out: uint16 bf16 bits or float32
+    array [rows, 1, C] (dim 1) / [rows, R, 1] (dim 2).  The value stored is the
+    bf16-rounded reduction (widened for a float32 out), as the reference
+    stores its bf16 result into the output.
+    """
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    loc = np.asarray(loc, dtype=np.int64)
+    P, H = int(page_size), int(num_kv_heads)
+    out = np.array(out, copy=True)
+    rows_out = out.shape[0]
+    trig = c_mod(loc + 1, P) == 0                     # reduce_impl.py:24
+    pages = c_div(loc[trig], P)                        # reduce_impl.py:26
+    rows = (pages[:, None] * H + np.arange(H)[None, :]).reshape(-1)
+    rows = rows[(rows >= 0) & (rows < x.shape[0]) & (rows < rows_out)]
+    rows = np.unique(rows)
+    axis = 1 if dim == 1 else 2
+    if rows.size:
+        t = x[rows]
+        if reduce_type == MEAN:
+            v = t.sum(axis=axis) / t.shape[axis]
+        elif reduce_type == MAX:
+            v = t.max(axis=axis)
+        elif reduce_type == MIN:
+            v = t.min(axis=axis)
+        elif reduce_type == L2NORM:
+            v = np.sqrt((t * t).sum(axis=axis))
+        else:
+            raise ValueError(f"unknown reduce type {reduce_type}")
+        bits = f32_to_bf16(v.astype(np.float32))
+        if dim == 1:
+            bits = bits[:, None, :]
+        else:
+            bits = bits[:, :, None]
+        if out.dtype == np.uint16:
+            out[rows] = bits
+        else:
+            out[rows] = bf16_to_f32(bits)
+    return out, rows
+
+
+# --------------------------------------------------------------------------
+# A.3 GeMV — indexer/triton_kernels/mv_impl.py:6-81
+# --------------------------------------------------------------------------
+
+
+def gemv(x_bits, y_bits, dense_indices, winfo_q, winfo_off, winfo_len, num_workloads: int,
+         out_len: int):
+    """Returns (scores as bf16 bits [out_len], covered mask [out_len])."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    y = bf16_to_f32(y_bits).astype(np.float64)
+    D = x.shape[-1]
+    x = x.reshape(-1, D)
+    y = y.reshape(-1, D)
+    dense = np.asarray(dense_indices, dtype=np.int64)
+    scores = np.zeros(out_len, dtype=np.uint16)
+    covered = np.zeros(out_len, dtype=bool)
+    nw = int(num_workloads)
+    if nw == 0:
+        return scores, covered
+    lens = np.asarray(winfo_len[:nw], dtype=np.int64)
+    offs = np.asarray(winfo_off[:nw], dtype=np.int64)
+    qs = np.asarray(winfo_q[:nw], dtype=np.int64)
+    # every covered position p with the query row of its workload
+    first = np.repeat(np.cumsum(lens) - lens, lens)
+    p = np.repeat(offs, lens) + (np.arange(int(lens.sum())) - first)
+    q = np.repeat(qs, lens)
+    v = np.einsum("ij,ij->i", y[dense[p]], x[q])
+    scores[p] = f32_to_bf16(v.astype(np.float32))
+    covered[p] = True
+    return scores, covered
+
+
+# --------------------------------------------------------------------------
+# A.4 topK — csrc/topk.cu:56-113 (host 117-203)
+# --------------------------------------------------------------------------
+
+
+def topk(score_bits, dense_indptr, sparse_indptr, dense_indices, sparse_indices,
+         eff_batch_size: int, topk_val: int, bos: int, eos: int):
+    """Returns (new_sparse_indices, written mask).
+
+    Per segment: stable descending sort of the middle scores (ties keep the
+    lower position first; -0.0 == +0.0), first topk_val dense indices written
+    after the BOS slots.  Segments with n <= topk_val are untouched.
+    """
+    sc = bf16_to_f32(score_bits).astype(np.float64)
+    dip = np.asarray(dense_indptr, dtype=np.int64)
+    sip = np.asarray(sparse_indptr, dtype=np.int64)
+    didx = np.asarray(dense_indices)
+    out = np.array(sparse_indices, copy=True)
+    written = np.zeros(out.shape[0], dtype=bool)
+    for s in range(int(eff_batch_size)):
+        start = dip[s] + bos
+        end = dip[s + 1] - eos
+        n = end - start
+        if n <= topk_val or topk_val <= 0:
+            continue
+        keys = sc[start:end] + 0.0            # folds -0.0 into +0.0
+        order = np.argsort(-keys, kind="stable")[:topk_val]
+        o0 = sip[s] + bos
+        out[o0:o0 + topk_val] = didx[start + order]
+        written[o0:o0 + topk_val] = True
+    return out, written
+
+
+# --------------------------------------------------------------------------
+# helper: the indexer pipeline of block_sparse_attention
+# (flow/algorithms.py:114-170)
+# --------------------------------------------------------------------------
+
+
+def q_group_mean(q_bits) -> np.ndarray:
+    """[S, G, D] bf16 bits -> [S, 1, D] bf16 bits (fp32-accurate mean)."""
+    q = bf16_to_f32(q_bits).astype(np.float64)
+    return f32_to_bf16(q.mean(axis=1, keepdims=True).astype(np.float32))

@@ -1,0 +1,219 @@
+"""GPU tests of the fused indexer kernel and of block_sparse_attention run
+through the public flow API (eager, fused and unfused, and replayed from a
+HIP graph).  Selections are bit-exact against the oracle's top-k of the same
+scores; scores and q-means are bit-exact against the separate kernels."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import workloads as W
+from oracle import vortex_oracle as O
+from vortex_torch import _hip
+from vortex_torch.abs import FORMAT, as_vtensor
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _bits(t):
+    with torch._C.DisableTorchFunctionSubclass():
+        return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+
+
+def _plan(batch, ic, dev):
+    from vortex_torch.indexer.utils_sglang import plan_decode
+
+    b = batch.to(dev)
+    plan_decode(b.seq_lens, b.req_to_token, b.req_indices, ic)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
+def test_fused_kernel_matches_separate_kernels(gpu, name):
+    dev = gpu
+    batch = getattr(W, name)()
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+    S = batch.batch * H
+    q = W.randn_bf16((S, G, D), 1, dev)
+    y = W.randn_bf16((batch.pool_pages * H, 1, D), 2, dev, std=0.25)
+    n_dense = ic.dense_kv_indices.numel()
+
+    # separate kernels: torch mean, GeMV, topK
+    qm_ref = q.mean(dim=1, keepdim=True)
+    sc_ref = torch.full((n_dense, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
+    _hip.gemv_paged(qm_ref, y, sc_ref, ic.dense_kv_indices, ic.winfo_q_indices, ic.winfo_kv_offsets,
+                    ic.winfo_kv_lens, ic.winfo_num_workloads, batch.max_chunk)
+    sp_ref = ic.sparse_kv_indices.clone()
+    _hip.topk_select(sc_ref, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp_ref,
+                     S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+
+    # fused
+    qm = torch.empty_like(qm_ref)
+    sc = torch.full_like(sc_ref, -5.0)
+    sp = ic.sparse_kv_indices.clone()
+    _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp,
+                       S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+    torch.cuda.synchronize()
+    if G in (1, 2, 4):
+        assert torch.equal(qm, qm_ref), "q-mean differs from torch.mean"
+    else:
+        np.testing.assert_allclose(O.bf16_to_f32(_bits(qm)), O.bf16_to_f32(_bits(qm_ref)), rtol=1e-2, atol=1e-3)
+    # same query -> same scores as the GeMV kernel, written at the same positions
+    sc_sep = torch.full_like(sc_ref, -5.0)
+    _hip.gemv_paged(qm, y, sc_sep, ic.dense_kv_indices, ic.winfo_q_indices, ic.winfo_kv_offsets,
+                    ic.winfo_kv_lens, ic.winfo_num_workloads, batch.max_chunk)
+    assert torch.equal(sc, sc_sep), "fused scores differ from the GeMV kernel"
+    # selection: oracle top-k of the fused kernel's own scores
+    exp, _ = O.topk(_bits(sc), _np(ic.dense_kv_indptr), _np(ic.sparse_kv_indptr), _np(ic.dense_kv_indices),
+                    _np(ic.sparse_kv_indices), S, batch.topk, batch.bos, batch.eos)
+    np.testing.assert_array_equal(_np(sp), exp)
+
+
+def test_fused_kernel_extra_query_rows(gpu):
+    # more query rows than segments (padded batch): every row gets its mean
+    dev = gpu
+    batch = W.c1()
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    S = batch.batch * batch.num_kv_heads
+    q = W.randn_bf16((S + 5, 2, 128), 3, dev)
+    y = W.randn_bf16((batch.pool_pages * batch.num_kv_heads, 1, 128), 4, dev)
+    qm = torch.empty((S + 5, 1, 128), device=dev, dtype=torch.bfloat16)
+    sc = torch.zeros((ic.dense_kv_indices.numel(), 1, 1), device=dev, dtype=torch.bfloat16)
+    _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices,
+                       ic.sparse_kv_indices, S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+    assert torch.equal(qm, q.mean(dim=1, keepdim=True))
+
+
+class _FlowRun:
+    """block_sparse_attention on one layer of `batch` through the public API."""
+
+    def __init__(self, batch, dev, seed=0):
+        from vortex_torch import flow as vflow
+
+        self.batch, self.dev = batch, dev
+        self.ic, self.cc = W.make_contexts(batch, dev)
+        H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+        self.flow = vflow.build_vflow("block_sparse_attention")
+        self.k = W.randn_bf16((batch.pool_pages * H, batch.page_size, D), seed, dev)
+        self.cen = W.randn_bf16((batch.pool_pages * H, 1, D), seed + 1, dev, std=0.25)
+        self.cache = {"k": as_vtensor(self.k, FORMAT.PAGED), "centroids": as_vtensor(self.cen, FORMAT.PAGED)}
+        self.q = as_vtensor(W.randn_bf16((batch.batch * H, G, D), seed + 2, dev), FORMAT.BATCHED)
+        self.o = as_vtensor(self.ic.sparse_kv_indices.view(-1, 1, 1), FORMAT.RAGGED)
+        self.loc = W.decode_loc(batch).to(dev)
+        self.dev_batch = batch.to(dev)  # no host copies inside a captured step
+        self.ic.profile()
+        self.cc.profile()
+        self.flow.forward_cache(self.cache, self.loc, self.cc)
+        self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
+        self.ic.execute()
+        self.cc.execute()
+
+    def step(self):
+        from vortex_torch.indexer.utils_sglang import plan_decode
+
+        b = self.dev_batch
+        plan_decode(b.seq_lens, b.req_to_token, b.req_indices, self.ic)
+        self.flow.forward_cache(self.cache, self.loc, self.cc)
+        self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
+def test_flow_fused_equals_unfused(gpu, name, monkeypatch):
+    batch = getattr(W, name)()
+    results = {}
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("VORTEX_FUSE", fuse)
+        run = _FlowRun(batch, gpu)
+        run.step()
+        torch.cuda.synchronize()
+        with torch._C.DisableTorchFunctionSubclass():
+            results[fuse] = (run.ic.sparse_kv_indices.clone(), run.flow.gemv.output_buffer.clone(),
+                             run.cen.clone())
+    assert torch.equal(results["1"][2], results["0"][2]), "centroids differ"
+    assert torch.equal(results["1"][0], results["0"][0]), "sparse indices differ"
+    # scores: compare the positions the GeMV covers (the planner's workloads)
+    ref = O.plan_decode(_np(batch.seq_lens), _np(batch.req_to_token), _np(batch.req_indices), batch.page_size,
+                        batch.num_kv_heads, batch.topk, batch.bos, batch.eos, batch.max_chunk)
+    cov = np.zeros(results["1"][1].numel(), dtype=bool)
+    for off, ln in zip(ref["winfo_off"], ref["winfo_len"]):
+        cov[off:off + ln] = True
+    np.testing.assert_array_equal(_bits(results["1"][1])[cov], _bits(results["0"][1])[cov])
+
+
+def test_flow_end_to_end_against_oracle(gpu):
+    batch = W.c2()
+    run = _FlowRun(batch, gpu, seed=5)
+    k_host = _bits(run.k).reshape(run.k.shape)
+    cen_before = _bits(run.cen).reshape(run.cen.shape)
+    run.step()
+    torch.cuda.synchronize()
+    H, P = batch.num_kv_heads, batch.page_size
+    ref = O.plan_decode(_np(batch.seq_lens), _np(batch.req_to_token), _np(batch.req_indices), P, H,
+                        batch.topk, batch.bos, batch.eos, batch.max_chunk)
+    # cache side: CMean of the pages the decode tokens close
+    cen_exp, rows = O.page_reduce(k_host, cen_before, _np(run.loc), H, P, 1, O.MEAN)
+    cen = _bits(run.cen).reshape(run.cen.shape)
+    np.testing.assert_allclose(O.bf16_to_f32(cen), O.bf16_to_f32(cen_exp), rtol=1e-2, atol=1e-3)
+    # indexer: scores within tolerance of the oracle, selection bit-exact on the GPU scores
+    qm = O.q_group_mean(_bits(run.q).reshape(tuple(run.q.shape)))
+    sc_exp, cov = O.gemv(qm, cen, ref["dense_indices"], ref["winfo_q"], ref["winfo_off"], ref["winfo_len"],
+                         ref["num_workloads"], run.flow.gemv.output_buffer.numel())
+    sc = _bits(run.flow.gemv.output_buffer)
+    np.testing.assert_allclose(O.bf16_to_f32(sc)[cov], O.bf16_to_f32(sc_exp)[cov], rtol=1e-2, atol=1e-3)
+    sel, _ = O.topk(sc, ref["dense_indptr"], ref["sparse_indptr"], ref["dense_indices"], ref["sparse_indices"],
+                    batch.batch * H, batch.topk, batch.bos, batch.eos)
+    np.testing.assert_array_equal(_np(run.ic.sparse_kv_indices), sel)
+
+
+def test_flow_graph_replay(gpu):
+    batch = W.c2()
+    run = _FlowRun(batch, gpu, seed=9)
+    stream = torch.cuda.Stream(gpu)
+    stream.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(stream):
+        run.step()
+    torch.cuda.synchronize()
+    with torch._C.DisableTorchFunctionSubclass():
+        eager_o = run.ic.sparse_kv_indices.clone()
+        eager_s = run.flow.gemv.output_buffer.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run.step()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        # eager work between replays, then clobber the outputs
+        run.ic.sparse_kv_indices.fill_(-3)
+        with torch._C.DisableTorchFunctionSubclass():
+            run.flow.gemv.output_buffer.fill_(0.5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        with torch._C.DisableTorchFunctionSubclass():
+            assert torch.equal(run.ic.sparse_kv_indices, eager_o), f"replay {rep}: selection differs"
+            s = run.flow.gemv.output_buffer
+            assert torch.equal(s[s != 0.5], eager_s[s != 0.5])
+
+
+def test_deferred_mean_materializes_on_use(gpu):
+    """A recorded q-mean read by other torch code sees torch.mean's result."""
+    from vortex_torch import _deferred
+
+    q = as_vtensor(W.randn_bf16((16, 2, 128), 7, gpu), FORMAT.BATCHED)
+    with _deferred.scope(True):
+        m = q.mean(dim=1, keepdim=True)
+        assert isinstance(m, _deferred.DeferredTensor) and m.is_pending
+        assert tuple(m.shape) == (16, 1, 128)  # metadata does not materialise
+        assert m.is_pending
+        doubled = m * 2
+        assert not m.is_pending
+    with torch._C.DisableTorchFunctionSubclass():
+        expect = q.as_subclass(torch.Tensor).mean(dim=1, keepdim=True)
+        assert torch.equal(m.as_subclass(torch.Tensor), expect)
+        assert torch.equal(doubled.as_subclass(torch.Tensor), expect * 2)

@@ -1,0 +1,87 @@
+// Device-side helpers shared by the gfx950 kernels: bf16 bit conversions,
+// order-preserving score keys, wave64 reductions/scans, error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/vortex_hip.h"
+
+namespace vtx {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 bits
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+// Low / high bf16 of a packed 32-bit word, widened to fp32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+  return __uint_as_float(w & 0xffff0000u);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (the integer-add formulation:
+// add 0x7fff plus the lowest kept bit, truncate).  Every NaN becomes the
+// quiet NaN 0x7fc0, as in torch's conversion.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Maps a bf16 bit pattern to a 16-bit unsigned key whose unsigned order is
+// the numeric order of the scores; -0.0 and +0.0 map to the same key.
+__device__ __forceinline__ uint32_t score_key(uint32_t bits16) {
+  bits16 &= 0xffffu;
+  if (bits16 == 0x8000u) bits16 = 0u;
+  return (bits16 & 0x8000u) ? (~bits16 & 0xffffu) : (bits16 | 0x8000u);
+}
+
+// ------------------------------------------------------------ wave helpers
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Number of set bits of `mask` in lanes strictly below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Treat a value as wave-uniform (moves it to a scalar register).
+__device__ __forceinline__ int uniform(int v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// Inclusive suffix sum over lanes: lane l gets sum of v over lanes >= l.
+__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    uint32_t o = __shfl_down(v, d, kWave);
+    if (l + d < kWave) v += o;
+  }
+  return v;
+}
+
+// 16-byte vector load/store of raw words.
+struct alignas(16) U4 {
+  uint32_t x, y, z, w;
+};
+__device__ __forceinline__ U4 ld16(const void* p) {
+  return *reinterpret_cast<const U4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, const U4& v) {
+  *reinterpret_cast<U4*>(p) = v;
+}
+
+}  // namespace vtx

@@ -1,0 +1,157 @@
+// Workgroup-wide top-k selection over 16-bit order keys (see score_key).
+//
+// select_topk() finds the k best of n items — largest key first, ties to the
+// lower position — and stores their composites (key << 32 | ~position) in
+// `sel[0..k)`, unordered.  rank_of() then gives a winner's output rank.
+//
+//   1. two 8-bit radix-histogram passes in LDS find the key `thr` of the k-th
+//      best item, the number of items above it and how many of the items
+//      equal to it are needed (`take`);
+//   2. items above `thr` win; items equal to `thr` win in position order
+//      (ballot + per-wave counts, tile by tile) until `take` are in.
+//
+// Every thread of the workgroup must call it (it contains barriers).
+#pragma once
+
+#include "vtx_device.h"
+
+namespace vtx {
+
+template <int T>
+struct SelectShared {
+  alignas(16) uint32_t hist[2][256];  // read 16 bytes per lane in sel_find_bin
+  uint32_t wave_ties[T / kWave];
+  int bin[2];
+  int above[2];
+  int count;
+};
+
+__device__ __forceinline__ uint64_t sel_composite(uint32_t key, long long pos) {
+  return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)pos);
+}
+__device__ __forceinline__ long long sel_position(uint64_t c) {
+  return (long long)(0xffffffffu - (uint32_t)c);
+}
+
+// Run by one full wave: the bin b of `hist` (256 bins, higher = better)
+// holding the kt-th best item, i.e. above(b) < kt <= above(b) + hist[b].
+__device__ __forceinline__ void sel_find_bin(const uint32_t* hist, uint32_t kt, int* bin, int* above_out) {
+  const int l = lane_id();
+  const U4 c = ld16(hist + 4 * l);
+  const uint32_t tot = c.x + c.y + c.z + c.w;
+  const uint32_t a3 = wave_suffix_sum(tot) - tot;
+  const uint32_t a2 = a3 + c.w;
+  const uint32_t a1 = a2 + c.z;
+  const uint32_t a0 = a1 + c.y;
+  if (a3 < kt && kt <= a2) {
+    *bin = 4 * l + 3;
+    *above_out = (int)a3;
+  } else if (a2 < kt && kt <= a1) {
+    *bin = 4 * l + 2;
+    *above_out = (int)a2;
+  } else if (a1 < kt && kt <= a0) {
+    *bin = 4 * l + 1;
+    *above_out = (int)a1;
+  } else if (a0 < kt && kt <= a0 + c.x) {
+    *bin = 4 * l;
+    *above_out = (int)a0;
+  }
+}
+
+// Clears the histograms, the winner count and the winner slots (no barrier).
+template <int T>
+__device__ __forceinline__ void select_init(uint64_t* sel, int k, SelectShared<T>& sh) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 256; i += T) {
+    sh.hist[0][i] = 0u;
+    sh.hist[1][i] = 0u;
+  }
+  if (tid == 0) sh.count = 0;
+  for (int j = tid; j < k; j += T) sel[j] = 0;  // decodes to a position >= n
+}
+
+// Adds one item to the high-byte histogram (callers that produce the keys
+// themselves build it on the fly and then call select_topk_counted).
+template <int T>
+__device__ __forceinline__ void select_count(uint32_t key, SelectShared<T>& sh) {
+  atomicAdd(&sh.hist[0][key >> 8], 1u);
+}
+
+// The selection once hist[0] holds every item (and a barrier made it visible).
+template <int T, typename KeyAt>
+__device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, int k, uint64_t* sel,
+                                                    SelectShared<T>& sh) {
+  constexpr int kWaves = T / kWave;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+
+  if (wave == 0) sel_find_bin(sh.hist[0], (uint32_t)k, &sh.bin[0], &sh.above[0]);
+  __syncthreads();
+  const uint32_t hi = (uint32_t)sh.bin[0];
+  const int above_hi = sh.above[0];
+
+  for (long long i = tid; i < n; i += T) {
+    const uint32_t key = key_at(i);
+    if ((key >> 8) == hi) atomicAdd(&sh.hist[1][key & 255u], 1u);
+  }
+  __syncthreads();
+  if (wave == 0) sel_find_bin(sh.hist[1], (uint32_t)(k - above_hi), &sh.bin[1], &sh.above[1]);
+  __syncthreads();
+  const uint32_t thr = (hi << 8) | (uint32_t)sh.bin[1];
+  const int take = k - (above_hi + sh.above[1]);  // >= 1 items equal to thr win
+  const bool all_ties = (take == (int)sh.hist[1][thr & 255u]);
+
+  for (long long i = tid; i < n; i += T) {
+    const uint32_t key = key_at(i);
+    if (key > thr || (all_ties && key == thr)) {
+      const int slot = atomicAdd(&sh.count, 1);
+      if (slot < k) sel[slot] = sel_composite(key, i);
+    }
+  }
+  if (!all_ties) {
+    int seen = 0;  // tied items in earlier tiles
+    for (long long t0 = 0; t0 < n; t0 += T) {
+      const long long i = t0 + tid;
+      const bool eq = (i < n) && key_at(i) == thr;
+      const uint64_t m = __ballot(eq);
+      if (lane == 0) sh.wave_ties[wave] = (uint32_t)__popcll(m);
+      __syncthreads();
+      int before = seen, tile = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const int c = (int)sh.wave_ties[w];
+        before += (w < wave) ? c : 0;
+        tile += c;
+      }
+      if (eq && before + lanes_below(m) < take) {
+        const int slot = atomicAdd(&sh.count, 1);
+        if (slot < k) sel[slot] = sel_composite(thr, i);
+      }
+      seen += tile;
+      __syncthreads();
+      if (seen >= take) break;
+    }
+  }
+  __syncthreads();
+}
+
+// key_at(i) returns the order key of item i < n.  Requires 0 < k < n.
+template <int T, typename KeyAt>
+__device__ __forceinline__ void select_topk(KeyAt key_at, long long n, int k, uint64_t* sel,
+                                            SelectShared<T>& sh) {
+  select_init<T>(sel, k, sh);
+  __syncthreads();
+  for (long long i = threadIdx.x; i < n; i += T) select_count<T>(key_at(i), sh);
+  __syncthreads();
+  select_topk_counted<T>(key_at, n, k, sel, sh);
+}
+
+// Output rank of winner `c` among the k winners in sel (best = 0).
+__device__ __forceinline__ int rank_of(uint64_t c, const uint64_t* sel, int k) {
+  int r = 0;
+  for (int m = 0; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
+  return r;
+}
+
+}  // namespace vtx

@@ -1,0 +1,227 @@
+"""Deferred execution inside a flow's ``forward_indexer``.
+
+A flow such as ``block_sparse_attention`` runs, per layer,
+``q.mean(1, keepdim=True)`` -> ``GeMV`` -> ``topK``.  Launched one by one,
+each of these costs a kernel launch plus a chain of dependent memory round
+trips, which at decode batch sizes is most of the layer's time.  Inside an
+execute-mode ``forward_indexer`` (a *scope*) the first two are recorded
+instead of launched:
+
+* ``q.mean(dim=1, keepdim=True)`` on a BATCHED bf16 GPU vTensor returns a
+  :class:`DeferredTensor` whose storage is allocated but not yet written;
+* ``GeMV`` returns its output buffer as a DeferredTensor;
+* ``topK`` on a deferred GeMV result launches one fused kernel that computes
+  the mean, the scores and the selection, writing all three results.
+
+Anything else materialises first: a torch operation on any vTensor inside the
+scope flushes all pending work (so no input can change under a recorded
+computation), a DeferredTensor used after the scope is already materialised,
+and leaving the scope flushes whatever is still pending.  Metadata queries
+(shape, dtype, device, ...) do not flush.  The results are the ones the
+separate ops produce; set ``VORTEX_FUSE=0`` to launch every op on its own.
+"""
+from __future__ import annotations
+
+import contextlib
+import os
+import threading
+from typing import List, Optional
+
+import torch
+
+_tls = threading.local()
+
+# Tensor queries that never read the data.
+_METADATA = {
+    torch.Tensor.dim,
+    torch.Tensor.size,
+    torch.Tensor.numel,
+    torch.Tensor.nelement,
+    torch.Tensor.is_contiguous,
+    torch.Tensor.element_size,
+    torch.Tensor.stride,
+    torch.Tensor.storage_offset,
+    torch.Tensor.get_device,
+    torch.Tensor.__len__,
+    torch.Tensor.shape.__get__,
+    torch.Tensor.dtype.__get__,
+    torch.Tensor.device.__get__,
+    torch.Tensor.ndim.__get__,
+    torch.Tensor.is_cuda.__get__,
+    torch.Tensor.layout.__get__,
+    torch.Tensor.requires_grad.__get__,
+}
+
+
+def fusion_enabled() -> bool:
+    return os.environ.get("VORTEX_FUSE", "1") != "0"
+
+
+class Pending:
+    """A recorded computation that writes a tensor's storage when flushed."""
+
+    def __init__(self):
+        self.done = False
+
+    def flush(self) -> None:
+        if not self.done:
+            self.done = True
+            self._run()
+
+    def _run(self) -> None:  # pragma: no cover - subclasses
+        raise NotImplementedError
+
+
+class PendingMean(Pending):
+    """``out = q.mean(dim=1, keepdim=True)`` (q: [S, G, D] bf16)."""
+
+    def __init__(self, q: torch.Tensor, out: torch.Tensor):
+        super().__init__()
+        self.q = q
+        self.out = out
+
+    def _run(self) -> None:
+        torch.mean(self.q, dim=1, keepdim=True, out=self.out)
+
+
+class Scope:
+    def __init__(self):
+        self.pending: List[Pending] = []
+
+    def add(self, p: Pending) -> None:
+        self.pending.append(p)
+
+    def flush(self) -> None:
+        while self.pending:
+            self.pending.pop(0).flush()
+
+
+def current_scope() -> Optional[Scope]:
+    return getattr(_tls, "scope", None)
+
+
+@contextlib.contextmanager
+def scope(active: bool):
+    """Deferral scope; flushes everything still pending on exit."""
+    prev = current_scope()
+    sc = Scope() if active else None
+    _tls.scope = sc
+    try:
+        yield sc
+    finally:
+        _tls.scope = prev
+        if sc is not None:
+            sc.flush()
+
+
+def flush_all() -> None:
+    sc = current_scope()
+    if sc is not None:
+        sc.flush()
+
+
+def is_metadata(func) -> bool:
+    return func in _METADATA
+
+
+def _mean_dim_args(args, kwargs):
+    """(dim, keepdim) of a mean call, or None if it has other arguments."""
+    rest = list(args[1:])
+    kw = dict(kwargs)
+    dim = kw.pop("dim", rest.pop(0) if rest else None)
+    keepdim = kw.pop("keepdim", rest.pop(0) if rest else False)
+    if rest or kw:
+        return None
+    if isinstance(dim, (tuple, list)):
+        if len(dim) != 1:
+            return None
+        dim = dim[0]
+    return dim, keepdim
+
+
+def try_defer_mean(func, args, kwargs):
+    """Records ``q.mean(dim=1, keepdim=True)`` of a BATCHED bf16 GPU vTensor
+    and returns the DeferredTensor, or None if the call is anything else."""
+    from .abs.tensor import FORMAT, vTensor
+
+    if func not in (torch.Tensor.mean, torch.mean) or not args:
+        return None
+    q = args[0]
+    if type(q) is not vTensor or q._format != FORMAT.BATCHED:
+        return None
+    parsed = _mean_dim_args(args, kwargs)
+    if parsed is None:
+        return None
+    dim, keepdim = parsed
+    with torch._C.DisableTorchFunctionSubclass():
+        if not (q.is_cuda and q.dtype == torch.bfloat16 and q.dim() == 3 and q.is_contiguous()):
+            return None
+        if dim not in (1, -2) or keepdim is not True:
+            return None
+        qp = q.as_subclass(torch.Tensor)
+        out = torch.empty((qp.shape[0], 1, qp.shape[2]), dtype=qp.dtype, device=qp.device)
+    p = PendingMean(qp, out)
+    current_scope().add(p)
+    return DeferredTensor.make(out, FORMAT.BATCHED, p)
+
+
+def _make_deferred_class():
+    from .abs.tensor import vTensor
+
+    class DeferredTensor(vTensor):
+        """A vTensor whose contents are produced by a recorded computation."""
+
+        _pending: Pending
+
+        @classmethod
+        def make(cls, base: torch.Tensor, fmt, pending: Pending) -> "DeferredTensor":
+            out = torch.Tensor._make_subclass(cls, base, require_grad=False)
+            out._format = fmt
+            out._pending = pending
+            return out
+
+        def materialize(self) -> None:
+            self._pending.flush()
+
+        @property
+        def is_pending(self) -> bool:
+            return not self._pending.done
+
+        @classmethod
+        def __torch_function__(cls, func, types, args=(), kwargs=None):
+            if not is_metadata(func):
+                flush_all()
+                for t in _iter_deferred((args, kwargs or {})):
+                    t._pending.flush()
+            return vTensor.__torch_function__.__func__(vTensor, func, types, args, kwargs)
+
+    return DeferredTensor
+
+
+def _iter_deferred(obj):
+    if isinstance(obj, DeferredTensor):
+        yield obj
+    elif isinstance(obj, (list, tuple)):
+        for x in obj:
+            yield from _iter_deferred(x)
+    elif isinstance(obj, dict):
+        for x in obj.values():
+            yield from _iter_deferred(x)
+
+
+DeferredTensor = _make_deferred_class()
+
+
+def pending_of(t) -> Optional[Pending]:
+    """The unflushed computation behind `t`, if any."""
+    if isinstance(t, DeferredTensor) and not t._pending.done:
+        return t._pending
+    return None
+
+
+def materialize(t):
+    """Flushes `t`'s computation (if deferred) and returns `t`."""
+    p = pending_of(t)
+    if p is not None:
+        p.flush()
+    return t

@@ -1,0 +1,438 @@
+"""ctypes binding of the gfx950 kernel library (C ABI in ``include/vortex_hip.h``).
+
+Every wrapper validates dtypes, devices, contiguity and sizes of its torch
+tensors, then launches on torch's current HIP stream of the tensors' device.
+Nothing here synchronises, reads device memory or allocates, so the wrappers
+can be recorded into a HIP graph (``torch.cuda.graph``).
+
+There is no CPU fallback: a tensor that is not on a GPU, or a missing
+library, raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libvortex_hip.so"
+_lock = threading.Lock()
+_lib = None
+
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+# Exported symbol -> argument types (order of include/vortex_hip.h).
+_SIGNATURES = {
+    "vtx_last_error": ([], ctypes.c_char_p),
+    "vtx_version": ([], ctypes.c_char_p),
+    "vtx_plan_decode": (
+        [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp,
+         _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_gemv_paged": (
+        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_topk_select": (
+        [_vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_page_reduce": (
+        [_vp, _i64, _i32, _i32, _vp, _i32, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_page_reduce_multi": (
+        [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_indexer_fused": (
+        [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+REDUCE_MEAN, REDUCE_MAX, REDUCE_MIN, REDUCE_L2NORM = 0, 1, 2, 3
+DTYPE_BF16, DTYPE_F32 = 0, 1
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Loads (once) and returns the kernel library; raises if it is missing."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = Path(path) if path is not None else _LIB_PATH
+        if not p.exists():
+            raise RuntimeError(
+                f"vortex_torch: kernel library not found at {p}; build it with "
+                "`python vortex_torch-dev_amd/build_native.py` (or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_LOCAL)
+        for name, (argtypes, restype) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def _plain(t):
+    """The same tensor without its subclass: layout-tagged and deferred tensors
+    are passed to the kernels by pointer, without running their torch hooks."""
+    if isinstance(t, torch.Tensor) and type(t) is not torch.Tensor:
+        with torch._C.DisableTorchFunctionSubclass():
+            return t.as_subclass(torch.Tensor)
+    if isinstance(t, (list, tuple)):
+        return type(t)(_plain(x) for x in t)
+    return t
+
+
+def _plain_args(fn):
+    import functools
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        return fn(*[_plain(a) for a in args], **{k: _plain(v) for k, v in kwargs.items()})
+
+    return wrapper
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _lib.vtx_last_error().decode(errors="replace") if _lib is not None else ""
+        raise RuntimeError(f"vortex_torch HIP {what} failed (code {rc}): {msg}")
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"vortex_torch: HIP kernels need GPU tensors, got a tensor on {t.device} "
+                "(there is no CPU implementation)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"vortex_torch: tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def _req(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if t.dtype != dtype:
+        raise RuntimeError(f"vortex_torch: {name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"vortex_torch: {name} must be contiguous")
+    return t
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class _on_device:
+    """Makes `dev` current for the duration of a launch (no-op if it already is)."""
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        idx = self.dev.index if self.dev.index is not None else cur
+        if idx != cur:
+            self.prev = cur
+            torch.cuda.set_device(idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+# ----------------------------------------------------------------------------
+# entry points
+# ----------------------------------------------------------------------------
+@_plain_args
+def plan_decode(
+    cached_seq_lens: torch.Tensor,
+    dense_kv_indptr: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    sparse_kv_indptr: torch.Tensor,
+    sparse_kv_indices: torch.Tensor,
+    kv_last_page_len: torch.Tensor,
+    req_to_token: torch.Tensor,
+    req_indices: torch.Tensor,
+    winfo_q_indices: torch.Tensor,
+    winfo_kv_offsets: torch.Tensor,
+    winfo_kv_lens: torch.Tensor,
+    winfo_num_workloads: torch.Tensor,
+    winfo_chunk_size: torch.Tensor,
+    page_size: int,
+    num_kv_heads: int,
+    topk_val: int,
+    page_reserved_bos: int,
+    page_reserved_eos: int,
+    max_chunk_size: int,
+    min_chunk_size: int,
+) -> None:
+    lib = load_library()
+    i32 = torch.int32
+    dev = _require_gpu(cached_seq_lens, dense_kv_indptr, dense_kv_indices, sparse_kv_indptr,
+                       sparse_kv_indices, kv_last_page_len, req_to_token, req_indices,
+                       winfo_q_indices, winfo_kv_offsets, winfo_kv_lens, winfo_num_workloads,
+                       winfo_chunk_size)
+    for t, n in ((cached_seq_lens, "cached_seq_lens"), (dense_kv_indptr, "dense_kv_indptr"),
+                 (dense_kv_indices, "dense_kv_indices"), (sparse_kv_indptr, "sparse_kv_indptr"),
+                 (sparse_kv_indices, "sparse_kv_indices"), (kv_last_page_len, "kv_last_page_len"),
+                 (req_to_token, "req_to_token"), (winfo_q_indices, "winfo_q_indices"),
+                 (winfo_kv_offsets, "winfo_kv_offsets"), (winfo_kv_lens, "winfo_kv_lens"),
+                 (winfo_num_workloads, "winfo_num_workloads"), (winfo_chunk_size, "winfo_chunk_size")):
+        _req(t, i32, n)
+    _req(req_indices, torch.int64, "req_indices")
+    B = int(cached_seq_lens.shape[0])
+    H = int(num_kv_heads)
+    if req_to_token.dim() != 2:
+        raise RuntimeError("vortex_torch: req_to_token must be 2-D [rows, max_tokens]")
+    if req_indices.numel() < B:
+        raise RuntimeError("vortex_torch: req_indices shorter than cached_seq_lens")
+    if dense_kv_indptr.numel() < B * H + 1 or sparse_kv_indptr.numel() < B * H + 1:
+        raise RuntimeError(f"vortex_torch: indptr buffers need {B * H + 1} entries")
+    if kv_last_page_len.numel() < B * H:
+        raise RuntimeError(f"vortex_torch: kv_last_page_len needs {B * H} entries")
+    if winfo_num_workloads.numel() < 1 or winfo_chunk_size.numel() < 1:
+        raise RuntimeError("vortex_torch: winfo_num_workloads / winfo_chunk_size need 1 entry")
+    wcap = min(winfo_q_indices.numel(), winfo_kv_offsets.numel(), winfo_kv_lens.numel())
+    with _on_device(dev):
+        rc = lib.vtx_plan_decode(
+            cached_seq_lens.data_ptr(), B,
+            dense_kv_indptr.data_ptr(), dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            sparse_kv_indptr.data_ptr(), sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
+            kv_last_page_len.data_ptr(),
+            req_to_token.data_ptr(), int(req_to_token.shape[0]), int(req_to_token.shape[1]),
+            req_indices.data_ptr(),
+            winfo_q_indices.data_ptr(), winfo_kv_offsets.data_ptr(), winfo_kv_lens.data_ptr(), wcap,
+            winfo_num_workloads.data_ptr(), winfo_chunk_size.data_ptr(),
+            int(page_size), H, int(topk_val), int(page_reserved_bos), int(page_reserved_eos),
+            int(max_chunk_size), int(min_chunk_size), _stream(dev))
+    _check(rc, "plan_decode")
+
+
+@_plain_args
+def gemv_paged(
+    x: torch.Tensor,
+    y: torch.Tensor,
+    o: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    winfo_q_indices: torch.Tensor,
+    winfo_kv_offsets: torch.Tensor,
+    winfo_kv_lens: torch.Tensor,
+    winfo_num_workloads: torch.Tensor,
+    max_chunk_size: int,
+) -> None:
+    lib = load_library()
+    dev = _require_gpu(x, y, o, dense_kv_indices, winfo_q_indices, winfo_kv_offsets,
+                       winfo_kv_lens, winfo_num_workloads)
+    _req(x, torch.bfloat16, "x")
+    _req(y, torch.bfloat16, "y")
+    _req(o, torch.bfloat16, "o")
+    for t, n in ((dense_kv_indices, "dense_kv_indices"), (winfo_q_indices, "winfo_q_indices"),
+                 (winfo_kv_offsets, "winfo_kv_offsets"), (winfo_kv_lens, "winfo_kv_lens"),
+                 (winfo_num_workloads, "winfo_num_workloads")):
+        _req(t, torch.int32, n)
+    D = int(x.shape[-1])
+    if int(y.shape[-1]) != D:
+        raise RuntimeError(f"vortex_torch: GeMV head_dim mismatch ({D} vs {int(y.shape[-1])})")
+    wcap = min(winfo_q_indices.numel(), winfo_kv_offsets.numel(), winfo_kv_lens.numel())
+    with _on_device(dev):
+        rc = lib.vtx_gemv_paged(
+            x.data_ptr(), x.numel() // D, y.data_ptr(), y.numel() // D, o.data_ptr(), o.numel(),
+            dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            winfo_q_indices.data_ptr(), winfo_kv_offsets.data_ptr(), winfo_kv_lens.data_ptr(), wcap,
+            winfo_num_workloads.data_ptr(), D, int(max_chunk_size), _stream(dev))
+    _check(rc, "gemv_paged")
+
+
+@_plain_args
+def topk_select(
+    x: torch.Tensor,
+    dense_kv_indptr: torch.Tensor,
+    sparse_kv_indptr: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    sparse_kv_indices: torch.Tensor,
+    eff_batch_size: int,
+    topk_val: int,
+    reserved_bos: int,
+    reserved_eos: int,
+    max_num_pages: int,
+) -> None:
+    lib = load_library()
+    dev = _require_gpu(x, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices)
+    _req(x, torch.bfloat16, "x (scores)")
+    for t, n in ((dense_kv_indptr, "dense_kv_indptr"), (sparse_kv_indptr, "sparse_kv_indptr"),
+                 (dense_kv_indices, "dense_kv_indices"), (sparse_kv_indices, "sparse_kv_indices")):
+        _req(t, torch.int32, n)
+    eff = int(eff_batch_size)
+    if eff < 0:
+        raise RuntimeError("vortex_torch: eff_batch_size must be >= 0")
+    if dense_kv_indptr.numel() < eff + 1 or sparse_kv_indptr.numel() < eff + 1:
+        raise RuntimeError(f"vortex_torch: indptr buffers need {eff + 1} entries")
+    with _on_device(dev):
+        rc = lib.vtx_topk_select(
+            x.data_ptr(), x.numel(), dense_kv_indptr.data_ptr(), sparse_kv_indptr.data_ptr(),
+            dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
+            eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages),
+            _stream(dev))
+    _check(rc, "topk_select")
+
+
+_OUT_DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}
+
+
+def _reduce_geometry(x: torch.Tensor, out: torch.Tensor, dim: int):
+    if x.dim() != 3:
+        raise RuntimeError("vortex_torch: page reduce expects x of rank 3 [rows, R, C]")
+    rows, R, C = (int(s) for s in x.shape)
+    if dim == 1:
+        per_row = C
+    elif dim == 2:
+        per_row = R
+    else:
+        raise RuntimeError(f"vortex_torch: dim must be 1 or 2, got {dim}")
+    if out.numel() % max(per_row, 1) != 0:
+        raise RuntimeError("vortex_torch: page reduce output size is not a multiple of its row")
+    return rows, R, C, out.numel() // max(per_row, 1)
+
+
+@_plain_args
+def page_reduce(x: torch.Tensor, out: torch.Tensor, loc: torch.Tensor, num_kv_heads: int,
+                page_size: int, dim: int, reduce_type: int) -> None:
+    lib = load_library()
+    dev = _require_gpu(x, out, loc)
+    _req(x, torch.bfloat16, "x")
+    _req(loc, torch.int64, "loc")
+    if out.dtype not in _OUT_DTYPES:
+        raise RuntimeError(f"vortex_torch: reduce output must be bf16 or fp32, got {out.dtype}")
+    _req(out, out.dtype, "output")
+    rows, R, C, out_rows = _reduce_geometry(x, out, dim)
+    with _on_device(dev):
+        rc = lib.vtx_page_reduce(
+            x.data_ptr(), rows, R, C, out.data_ptr(), _OUT_DTYPES[out.dtype], out_rows,
+            loc.data_ptr(), loc.numel(), int(num_kv_heads), int(page_size), int(dim),
+            int(reduce_type), _stream(dev))
+    _check(rc, "page_reduce")
+
+
+@_plain_args
+def page_reduce_multi(x: torch.Tensor, outs, reduce_types, loc: torch.Tensor, num_kv_heads: int,
+                      page_size: int, dim: int = 1) -> None:
+    """One pass over every finished tile of x feeding up to four reductions."""
+    lib = load_library()
+    outs = list(outs)
+    reduce_types = [int(t) for t in reduce_types]
+    if not 1 <= len(outs) <= 4 or len(outs) != len(reduce_types):
+        raise RuntimeError("vortex_torch: page_reduce_multi needs 1..4 outputs, one type each")
+    dev = _require_gpu(x, loc, *outs)
+    _req(x, torch.bfloat16, "x")
+    _req(loc, torch.int64, "loc")
+    out_rows = None
+    for o in outs:
+        if o.dtype not in _OUT_DTYPES:
+            raise RuntimeError(f"vortex_torch: reduce output must be bf16 or fp32, got {o.dtype}")
+        _req(o, o.dtype, "output")
+        rows, R, C, r = _reduce_geometry(x, o, dim)
+        out_rows = r if out_rows is None else min(out_rows, r)
+    n = len(outs)
+    ptrs = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    dts = (ctypes.c_int32 * n)(*[_OUT_DTYPES[o.dtype] for o in outs])
+    tys = (ctypes.c_int32 * n)(*reduce_types)
+    with _on_device(dev):
+        rc = lib.vtx_page_reduce_multi(
+            x.data_ptr(), rows, R, C, n, ptrs, dts, tys, out_rows, loc.data_ptr(), loc.numel(),
+            int(num_kv_heads), int(page_size), int(dim), _stream(dev))
+    _check(rc, "page_reduce_multi")
+
+
+def indexer_fused_supported(head_dim: int) -> bool:
+    return bool(load_library().vtx_indexer_fused_supported(int(head_dim)))
+
+
+@_plain_args
+def indexer_fused(
+    q: torch.Tensor,
+    x_out,
+    y: torch.Tensor,
+    score: torch.Tensor,
+    dense_kv_indptr: torch.Tensor,
+    sparse_kv_indptr: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    sparse_kv_indices: torch.Tensor,
+    eff_batch_size: int,
+    topk_val: int,
+    reserved_bos: int,
+    reserved_eos: int,
+    max_num_pages: int,
+) -> None:
+    """q-mean + GeMV + topK of one layer in one launch.
+
+    q: bf16 [S, G, D] (the head-group mean is taken in the kernel and written
+    to x_out if given) or [S, 1, D] / [S, D] already-averaged rows (G taken as
+    0: rows used as they are).  y: centroid pool [rows, 1, D]; score: the GeMV
+    output buffer; the block tables come from the planner.
+    """
+    lib = load_library()
+    tensors = [q, y, score, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
+    if x_out is not None:
+        tensors.append(x_out)
+    dev = _require_gpu(*tensors)
+    _req(q, torch.bfloat16, "q")
+    _req(y, torch.bfloat16, "y (centroids)")
+    _req(score, torch.bfloat16, "score")
+    for t, n in ((dense_kv_indptr, "dense_kv_indptr"), (sparse_kv_indptr, "sparse_kv_indptr"),
+                 (dense_kv_indices, "dense_kv_indices"), (sparse_kv_indices, "sparse_kv_indices")):
+        _req(t, torch.int32, n)
+    D = int(q.shape[-1])
+    if int(y.shape[-1]) != D:
+        raise RuntimeError(f"vortex_torch: fused indexer head_dim mismatch ({D} vs {int(y.shape[-1])})")
+    eff = int(eff_batch_size)
+    G = int(q.shape[1]) if q.dim() == 3 else 1
+    S = q.numel() // (G * D)
+    if S < eff:
+        raise RuntimeError(f"vortex_torch: {S} query rows for {eff} segments")
+    if dense_kv_indptr.numel() < eff + 1 or sparse_kv_indptr.numel() < eff + 1:
+        raise RuntimeError(f"vortex_torch: indptr buffers need {eff + 1} entries")
+    if x_out is not None:
+        _req(x_out, torch.bfloat16, "x_out (q_mean)")
+        if x_out.numel() < S * D:
+            raise RuntimeError("vortex_torch: q_mean output too small")
+    averaged = G == 1 and x_out is None
+    with _on_device(dev):
+        rc = lib.vtx_indexer_fused(
+            None if averaged else q.data_ptr(), S, 0 if averaged else G,
+            q.data_ptr() if averaged else None,
+            x_out.data_ptr() if x_out is not None else None,
+            y.data_ptr(), y.numel() // D, score.data_ptr(), score.numel(),
+            dense_kv_indptr.data_ptr(), sparse_kv_indptr.data_ptr(),
+            dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
+            eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), D,
+            _stream(dev))
+    _check(rc, "indexer_fused")

@@ -1,0 +1,149 @@
+"""Indexer GeMV: scores every page of every segment against the segment's query.
+
+``GeMV()(x, y, ctx=ctx)`` with x ``[B*H_kv, 1, D]`` (BATCHED) and y the
+centroid pool ``[pool_rows, 1, D]`` (PAGED) returns a RAGGED score vector
+``[ctx.max_num_pages, 1, 1]`` of x's dtype, where for each planner workload
+(segment q, offset, length) ``score[p] = x[q] . y[dense_kv_indices[p]]``.
+Only the positions of the workloads (the middle pages of segments that need a
+top-k) are written.
+
+Profile / execute contract and checks follow the reference
+(vortex_torch/indexer/matmul.py:10-189).  The execute path launches the gfx950
+kernel of ``libvortex_hip.so`` (``vtx_gemv_paged``), or — inside a flow's
+forward_indexer, when a topK consumes the scores — records the launch so
+that the topK runs mean + GeMV + select as one kernel (``vtx_indexer_fused``).
+"""
+from __future__ import annotations
+
+from typing import Callable, Dict, Optional, Tuple
+
+import torch
+
+from .. import _deferred, _hip
+from ..abs import FORMAT, as_vtensor, vOp, vTensor
+from .context import Context
+
+
+class PendingGemv(_deferred.Pending):
+    """A recorded ``GeMV`` launch.  ``topK`` on its result replaces it (and
+    the recorded mean of its query, if any) by one fused launch."""
+
+    def __init__(self, op: "GeMV", x: torch.Tensor, y: torch.Tensor, ctx: Context):
+        super().__init__()
+        self.op, self.x, self.y, self.ctx = op, x, y, ctx
+
+    def _run(self) -> None:
+        _deferred.materialize(self.x)
+        self.op.impl(self.x, self.y, self.op.output_buffer, self.ctx)
+
+    def fuse_with_topk(self, o: torch.Tensor, ctx: Context) -> None:
+        """q-mean (if recorded) + GeMV + topK into ``o`` in one kernel."""
+        sc = _deferred.current_scope()
+        mean = _deferred.pending_of(self.x)
+        # earlier recorded work runs first, in program order
+        if sc is not None:
+            for p in list(sc.pending):
+                if p is mean or p is self:
+                    break
+                p.flush()
+        if isinstance(mean, _deferred.PendingMean):
+            q, x_out = mean.q, mean.out
+        else:
+            _deferred.materialize(self.x)
+            q, x_out = self.x, None
+        _hip.indexer_fused(
+            q, x_out, self.y, self.op.output_buffer,
+            ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
+            ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
+            ctx.page_reserved_eos, ctx.max_num_pages_per_request)
+        if mean is not None:
+            mean.done = True
+        self.done = True
+
+
+def _fusable(x: torch.Tensor, y: torch.Tensor, ctx: Context) -> bool:
+    """Whether GeMV may wait for a following topK to run fused with it.
+
+    The fused kernel scores each segment's middle pages from the block table
+    (dense_kv_indptr, bos, eos, topk) instead of walking the workload list;
+    both describe the same pages for a plan_decode block table as long as a
+    segment's middle count fits the planner's int16 (the reference caps
+    requests at 4096 pages, far below)."""
+    if _deferred.current_scope() is None or not _deferred.fusion_enabled():
+        return False
+    with torch._C.DisableTorchFunctionSubclass():
+        if not (x.is_cuda and y.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16):
+            return False
+        D = int(x.shape[-1])
+    try:
+        span = int(ctx.max_num_pages_per_request) - int(ctx.page_reserved_bos) - int(ctx.page_reserved_eos)
+        if span >= 32768 or int(ctx.topk_val) > 4096:
+            return False
+    except (TypeError, ValueError):
+        return False
+    return _hip.indexer_fused_supported(D)
+
+
+def mv_bpr(x: torch.Tensor, y: torch.Tensor, o: torch.Tensor, ctx: Context) -> None:
+    """(BATCHED x, PAGED y) -> RAGGED o, walking ctx's workload list."""
+    _hip.gemv_paged(
+        x, y, o,
+        ctx.dense_kv_indices,
+        ctx.winfo_q_indices,
+        ctx.winfo_kv_offsets,
+        ctx.winfo_kv_lens,
+        ctx.winfo_num_workloads,
+        ctx.max_chunk_size,
+    )
+
+
+class GeMV(vOp):
+    _impl_map: Dict[Tuple[FORMAT, FORMAT], Tuple[Callable, FORMAT]] = {
+        (FORMAT.BATCHED, FORMAT.PAGED): (mv_bpr, FORMAT.RAGGED),
+    }
+
+    def __init__(self):
+        super().__init__()
+        self.impl: Optional[Callable] = None
+        self.output_format: Optional[FORMAT] = None
+        self.output_buffer: Optional[torch.Tensor] = None
+
+    def profile(self, x: vTensor, y: vTensor, ctx: Context) -> vTensor:
+        p = self._prefix()
+        assert isinstance(x, vTensor), f"{p}profile expects x to be vTensor, got {type(x)}"
+        assert isinstance(y, vTensor), f"{p}profile expects y to be vTensor, got {type(y)}"
+        assert x.dim() == 3 and y.dim() == 3, (
+            f"{p}expected 3D inputs; got x.ndim={x.dim()}, y.ndim={y.dim()}")
+        assert x.shape[1] == 1, f"{p}expected x.shape[1] == 1, got {tuple(x.shape)}"
+        assert y.shape[1] == 1, f"{p}expected y.shape[1] == 1, got {tuple(y.shape)}"
+        assert x.shape[2] == y.shape[2], (
+            f"{p}last dimension mismatch: x.shape[2]={x.shape[2]} vs y.shape[2]={y.shape[2]}")
+        key = (x._format, y._format)
+        assert key in self._impl_map, (
+            f"{p}no implementation for (x_fmt={key[0]}, y_fmt={key[1]}). "
+            f"Available: {list(self._impl_map.keys())}")
+        self.impl, self.output_format = self._impl_map[key]
+
+        self.output_buffer = torch.empty((ctx.max_num_pages, 1, 1), device=x.device, dtype=x.dtype)
+        ctx.add_aux_memory(self.output_buffer)
+        for t in (x, y):
+            if t._format == FORMAT.PAGED:
+                ctx.add_aux_flops(t.shape[1] * t.shape[2])
+        return as_vtensor(self.output_buffer, self.output_format)
+
+    def execute(self, x: torch.Tensor, y: torch.Tensor, ctx: Context) -> torch.Tensor:
+        p = self._prefix()
+        assert self.impl is not None, f"{p}execute called before profile() (impl is None)"
+        assert self.output_buffer is not None, f"{p}output buffer is None; did profile() run?"
+        assert x.device == y.device == self.output_buffer.device, (
+            f"{p}device mismatch: x={x.device}, y={y.device}, o={self.output_buffer.device}")
+        if self.impl is mv_bpr and _fusable(x, y, ctx):
+            pending = PendingGemv(self, x, y, ctx)
+            _deferred.current_scope().add(pending)
+            return _deferred.DeferredTensor.make(self.output_buffer, self.output_format, pending)
+        _deferred.materialize(x)
+        self.impl(x, y, self.output_buffer, ctx)
+        return self.output_buffer
+
+
+__all__ = ["GeMV", "mv_bpr"]

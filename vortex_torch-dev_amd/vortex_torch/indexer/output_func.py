@@ -1,0 +1,74 @@
+"""Indexer topK: turns per-page scores into the sparse block table.
+
+``topK()(x, o, ctx=ctx)`` takes the RAGGED score vector ``[S, 1, 1]`` and
+writes, for every segment that has more than ``topk_val`` middle pages, the
+``topk_val`` best-scoring middle pages (best first, ties to the lower page
+position) into ``o`` after the segment's reserved BOS pages.  Segments with
+fewer middle pages are left as the planner wrote them (all pages).
+
+Profile / execute contract follows the reference
+(vortex_torch/indexer/output_func.py:8-235); execute calls ``topk_output``
+with the reference's argument list, which launches the gfx950 select kernel.
+When its input is a GeMV result recorded inside the same forward_indexer, it
+launches the fused mean + GeMV + select kernel instead.
+"""
+from __future__ import annotations
+
+from typing import Callable, Dict, Optional
+
+import torch
+
+from .. import _deferred
+from .._C import topk_output
+from ..abs import FORMAT, vOp, vTensor
+from .context import Context
+from .matmul import PendingGemv
+
+
+class topK(vOp):
+    _impl_map: Dict[FORMAT, Callable] = {
+        FORMAT.RAGGED: topk_output,
+    }
+
+    def __init__(self):
+        super().__init__()
+        self.impl: Optional[Callable] = None
+
+    def profile(self, x: vTensor, o: vTensor, ctx: Context) -> None:
+        p = self._prefix()
+        assert isinstance(x, vTensor), f"{p}profile expects x to be vTensor, got {type(x)}"
+        assert isinstance(o, vTensor), f"{p}profile expects o to be vTensor, got {type(o)}"
+        assert x.dim() == 3, f"{p}expected x to be 3D, got ndim={x.dim()} shape={tuple(x.shape)}"
+        assert o.dim() == 3, f"{p}expected o to be 3D, got ndim={o.dim()} shape={tuple(o.shape)}"
+        assert x.shape[1] == 1 and x.shape[2] == 1, (
+            f"{p}expected x.shape[1] == x.shape[2] == 1, got {tuple(x.shape)}")
+        assert x._format in self._impl_map, (
+            f"{p}no implementation for x._format={x._format}. "
+            f"Available: {list(self._impl_map.keys())}")
+        self.impl = self._impl_map[x._format]
+        assert x.device == o.device, (
+            f"{p}x and o must be on the same device (x.device={x.device}, o.device={o.device})")
+
+    def execute(self, x: torch.Tensor, o: torch.Tensor, ctx: Context) -> torch.Tensor:
+        assert self.impl is not None, f"{self._prefix()}execute called before profile() (impl is None)"
+        pending = _deferred.pending_of(x)
+        if self.impl is topk_output and isinstance(pending, PendingGemv) and pending.ctx is ctx:
+            pending.fuse_with_topk(o, ctx)
+            return o
+        _deferred.materialize(x)
+        self.impl(
+            x,
+            ctx.dense_kv_indptr,
+            ctx.sparse_kv_indptr,
+            ctx.dense_kv_indices,
+            o,
+            ctx.batch_size * ctx.num_kv_heads,
+            ctx.topk_val,
+            ctx.page_reserved_bos,
+            ctx.page_reserved_eos,
+            ctx.max_num_pages_per_request,
+        )
+        return o
+
+
+__all__ = ["topK"]

@@ -1,0 +1,74 @@
+"""Serving-runtime helpers of the indexer.
+
+``plan_decode`` is called once per decode step by the attention backend,
+before any layer runs: it fills the context's block tables and workload list
+(reference vortex_torch/indexer/utils_sglang.py:15-44).  The prefill, FA3 and
+transpose helpers of the reference serve other attention paths; they exist
+here under the same names and raise ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _C
+from .context import Context
+
+
+def plan_decode(
+    cached_seq_lens: torch.Tensor,
+    req_to_token: torch.Tensor,
+    req_indices: torch.Tensor,
+    ctx: Context,
+) -> None:
+    _C.sglang_plan_decode(
+        cached_seq_lens,
+        ctx.dense_kv_indptr,
+        ctx.dense_kv_indices,
+        ctx.sparse_kv_indptr,
+        ctx.sparse_kv_indices,
+        ctx.kv_last_page_len,
+        req_to_token,
+        req_indices,
+        ctx.winfo_q_indices,
+        ctx.winfo_kv_offsets,
+        ctx.winfo_kv_lens,
+        ctx.winfo_num_workloads,
+        ctx.winfo_chunk_size,
+        ctx.page_size,
+        ctx.num_kv_heads,
+        ctx.topk_val,
+        ctx.page_reserved_bos,
+        ctx.page_reserved_eos,
+        ctx.max_chunk_size,
+        ctx.min_chunk_size,
+    )
+    ctx.set_batch_size(cached_seq_lens.shape[0])
+
+
+def plan_prefill(*args, **kwargs):
+    return _C.sglang_plan_prefill(*args, **kwargs)
+
+
+def plan_prefill_fa3(*args, **kwargs):
+    return _C.sglang_plan_prefill_fa3(*args, **kwargs)
+
+
+def plan_decode_fa3(*args, **kwargs):
+    return _C.sglang_plan_decode_fa3(*args, **kwargs)
+
+
+def chunkwise_nh2hn_transpose(*args, **kwargs):
+    return _C.Chunkwise_NH2HN_Transpose(*args, **kwargs)
+
+
+def chunkwise_hn2nh_transpose(*args, **kwargs):
+    return _C.Chunkwise_HN2NH_Transpose(*args, **kwargs)
+
+
+def chunkwise_hn2nh_transpose_fa3(*args, **kwargs):
+    return _C.Chunkwise_HN2NH_Transpose_FA3(*args, **kwargs)
+
+
+def indices_to_page_table(page_table: torch.Tensor, ctx: Context) -> None:
+    """No-op, as in the reference (utils_sglang.py:190-193)."""
+    return None
