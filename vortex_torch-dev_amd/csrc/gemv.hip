@@ -52,19 +52,6 @@ __device__ __forceinline__ long long workload_count(const GemvArgs& a) {
   return nw;
 }
 
-__device__ __forceinline__ float dot16(const vtx::U4& v, const float* xs) {
-  float s = 0.f;
-  s = fmaf(vtx::bf16_lo(v.x), xs[0], s);
-  s = fmaf(vtx::bf16_hi(v.x), xs[1], s);
-  s = fmaf(vtx::bf16_lo(v.y), xs[2], s);
-  s = fmaf(vtx::bf16_hi(v.y), xs[3], s);
-  s = fmaf(vtx::bf16_lo(v.z), xs[4], s);
-  s = fmaf(vtx::bf16_hi(v.z), xs[5], s);
-  s = fmaf(vtx::bf16_lo(v.w), xs[6], s);
-  s = fmaf(vtx::bf16_hi(v.w), xs[7], s);
-  return s;
-}
-
 // LPR lanes per row, VPL 16-byte vectors per lane: dim == LPR * VPL * 8.
 template <int LPR, int VPL>
 __global__ __launch_bounds__(kThreads, (VPL == 1 ? 4 : 2)) void gemv_paged_kernel(GemvArgs a) {
@@ -165,9 +152,7 @@ __global__ __launch_bounds__(kThreads, (VPL == 1 ? 4 : 2)) void gemv_paged_kerne
         }
 #pragma unroll
         for (int ii = 0; ii < kBatch; ++ii) {
-          float s = 0.f;
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) s += dot16(buf[ii][v], xs[v]);
+          const float s = vtx::dot_row<VPL>(buf[ii], xs);
           acc[i0 + ii] = live[ii] ? s : 0.f;
         }
       }

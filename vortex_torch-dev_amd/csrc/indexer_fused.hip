@@ -13,14 +13,17 @@
 //
 // Why fused: at decode batch sizes each of the three kernels is dominated by
 // its launch and its chain of dependent memory round trips, not by bytes.
-// Here the chain is: segment bounds -> dense rows (into LDS) -> centroid rows
-// (the only bulk traffic, 2*D bytes per page) -> LDS select -> stores.  The
-// scores never leave the chip for the select and the winners' page ids come
-// from LDS.
+// Here the chain is: segment bounds -> one coalesced load of the pass's page
+// ids -> centroid rows (the only bulk traffic, 2*D bytes per page) -> LDS
+// select -> stores.  The scores never leave the chip for the select and,
+// for segments that fit the LDS row cache, neither do the winners' page ids.
 //
-// Row scoring uses the same geometry as gemv.hip: a wave handles 64 pages per
-// pass, LPR lanes x VPL 16-byte vectors per row, reduce-scatter so that each
-// lane ends with one finished score.
+// Row scoring: a segment's middle pages are split evenly over the waves, at
+// most kPass pages per wave pass (64 for rows of one 16-byte vector per lane,
+// 32 for wider rows), LPR lanes x VPL 16-byte vectors per row.  The per-lane
+// dot product (vtx::dot_row) and the reduce-scatter tree over the LPR lanes
+// are the ones gemv.hip uses, so the scores are bit-identical to the GeMV
+// kernel's for the same query.
 #include "vtx_device.h"
 #include "vtx_host.h"
 #include "vtx_select.h"
@@ -121,10 +124,10 @@ template <int T, int LPR, int VPL>
 __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
-  constexpr int kPass = 32;                        // pages per wave pass
+  constexpr int kPass = VPL == 1 ? 64 : 32;        // at most this many pages per wave pass
   constexpr int kSlots = kPass / kRowsPerLoad;     // pages per lane per pass
   constexpr int kBatch = VPL <= 2 ? kSlots : 2;    // slots loaded together
-  constexpr int kQRegs = VPL == 1 ? 4 : (VPL == 2 ? 2 : 1);  // query rows prefetched
+  constexpr int kQRegs = VPL <= 2 ? 2 : 1;         // query rows prefetched
   static_assert(kSlots >= 1 && kSlots <= LPR, "pass geometry");
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
@@ -178,22 +181,23 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   __syncthreads();  // histogram cleared before any wave counts into it
   bool have_mean = false;
 
-  // ---- 4. scores: each wave takes passes of kPass pages; row ids come
-  // straight from global memory (no barrier before the first centroid load)
+  // ---- 4. scores: the pages are split evenly over the waves (one pass
+  // each up to kWaves * kPass pages, so no wave waits on a second round
+  // trip while others idle); row ids come straight from global memory
   const int32_t* dseg = a.didx + start;
-  for (long long p0 = (long long)wave * kPass; p0 < n; p0 += (long long)kWaves * kPass) {
-    const int cnt = (int)min((long long)kPass, n - p0);
-    int rid[kSlots];
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
-      const int r = i * kRowsPerLoad + grp;
-      rid[i] = r < cnt ? dseg[p0 + r] : -1;
-    }
+  long long share = (n + kWaves - 1) / kWaves;
+  share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+  if (share > kPass) share = kPass;
+  for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
+    const int cnt = (int)min(share, n - p0);
+    // one coalesced load of the pass's row ids (lane l holds position l),
+    // handed to the lanes that need them with shuffles
+    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
     if (!have_mean) {
       query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, wave, grp, col, xs);
       have_mean = true;
     }
-    int first = __shfl(rid[0], 0, vtx::kWave);
+    int first = __shfl(my_row, 0, vtx::kWave);
     if (first < 0 || first >= a.y_rows) first = 0;
     float acc[kSlots];
 #pragma unroll
@@ -202,27 +206,20 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       bool live[kBatch];
 #pragma unroll
       for (int ii = 0; ii < kBatch; ++ii) {
-        const int row = rid[i0 + ii];
+        const int row = __shfl(my_row, (i0 + ii) * kRowsPerLoad + grp, vtx::kWave);
         live[ii] = row >= 0 && row < a.y_rows;
-        const uint16_t* yr = a.y + (long long)(live[ii] ? row : first) * D;
+        if ((i0 + ii) * kRowsPerLoad < cnt) {  // wave-uniform: slots past the share are skipped
+          const uint16_t* yr = a.y + (long long)(live[ii] ? row : first) * D;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16(yr + (v * LPR + col) * 8);
+          for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16(yr + (v * LPR + col) * 8);
+        } else {
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::U4{0u, 0u, 0u, 0u};
+        }
       }
 #pragma unroll
       for (int ii = 0; ii < kBatch; ++ii) {
-        float s = 0.f;
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) {
-          const vtx::U4& w = buf[ii][v];
-          s = fmaf(vtx::bf16_lo(w.x), xs[v][0], s);
-          s = fmaf(vtx::bf16_hi(w.x), xs[v][1], s);
-          s = fmaf(vtx::bf16_lo(w.y), xs[v][2], s);
-          s = fmaf(vtx::bf16_hi(w.y), xs[v][3], s);
-          s = fmaf(vtx::bf16_lo(w.z), xs[v][4], s);
-          s = fmaf(vtx::bf16_hi(w.z), xs[v][5], s);
-          s = fmaf(vtx::bf16_lo(w.w), xs[v][6], s);
-          s = fmaf(vtx::bf16_hi(w.w), xs[v][7], s);
-        }
+        const float s = vtx::dot_row<VPL>(buf[ii], xs);
         acc[i0 + ii] = live[ii] ? s : 0.f;
       }
     }
@@ -243,10 +240,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     for (int d = 1; d < kShare; d <<= 1) acc[0] += __shfl_xor(acc[0], d, vtx::kWave);
     const int slot = col / kShare;
     const int r = slot * kRowsPerLoad + grp;
-    int my_rid = rid[0];  // rid[slot] without indexing a register array
-#pragma unroll
-    for (int i = 1; i < kSlots; ++i)
-      if (i == slot) my_rid = rid[i];
+    const int my_rid = __shfl(my_row, r, vtx::kWave);  // row id of this lane's page
     if ((col % kShare) == 0 && r < cnt) {
       const uint32_t sb = vtx::f32_to_bf16(acc[0]);
       const uint32_t key = vtx::score_key(sb);

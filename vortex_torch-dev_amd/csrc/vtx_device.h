@@ -84,4 +84,36 @@ __device__ __forceinline__ void st16(void* p, const U4& v) {
   *reinterpret_cast<U4*>(p) = v;
 }
 
+// Widens 8 packed bf16 values to fp32.
+__device__ __forceinline__ void unpack8(const U4& t, float* f) {
+  f[0] = bf16_lo(t.x);
+  f[1] = bf16_hi(t.x);
+  f[2] = bf16_lo(t.y);
+  f[3] = bf16_hi(t.y);
+  f[4] = bf16_lo(t.z);
+  f[5] = bf16_hi(t.z);
+  f[6] = bf16_lo(t.w);
+  f[7] = bf16_hi(t.w);
+}
+
+// This lane's share of a row dot product: VPL vectors of 8 bf16 against the
+// fp32 query slice, one fused multiply-add chain in column order.  Every
+// scoring kernel uses it, so their scores agree bit for bit.
+template <int VPL>
+__device__ __forceinline__ float dot_row(const U4 (&w)[VPL], const float (&xs)[VPL][8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    s = fmaf(bf16_lo(w[v].x), xs[v][0], s);
+    s = fmaf(bf16_hi(w[v].x), xs[v][1], s);
+    s = fmaf(bf16_lo(w[v].y), xs[v][2], s);
+    s = fmaf(bf16_hi(w[v].y), xs[v][3], s);
+    s = fmaf(bf16_lo(w[v].z), xs[v][4], s);
+    s = fmaf(bf16_hi(w[v].z), xs[v][5], s);
+    s = fmaf(bf16_lo(w[v].w), xs[v][6], s);
+    s = fmaf(bf16_hi(w[v].w), xs[v][7], s);
+  }
+  return s;
+}
+
 }  // namespace vtx

@@ -19,10 +19,8 @@ namespace vtx {
 
 template <int T>
 struct SelectShared {
-  alignas(16) uint32_t hist[2][256];  // read 16 bytes per lane in sel_find_bin
+  alignas(16) uint32_t hist[2][256];  // read 16 bytes per lane in sel_find_bin_wave
   uint32_t wave_ties[T / kWave];
-  int bin[2];
-  int above[2];
   int count;
 };
 
@@ -33,9 +31,10 @@ __device__ __forceinline__ long long sel_position(uint64_t c) {
   return (long long)(0xffffffffu - (uint32_t)c);
 }
 
-// Run by one full wave: the bin b of `hist` (256 bins, higher = better)
-// holding the kt-th best item, i.e. above(b) < kt <= above(b) + hist[b].
-__device__ __forceinline__ void sel_find_bin(const uint32_t* hist, uint32_t kt, int* bin, int* above_out) {
+// Run by one full wave (every lane gets the answer): the bin b of `hist`
+// (256 bins, higher = better) holding the kt-th best item, i.e.
+// above(b) < kt <= above(b) + hist[b], and above(b).
+__device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t kt, int* bin, int* above) {
   const int l = lane_id();
   const U4 c = ld16(hist + 4 * l);
   const uint32_t tot = c.x + c.y + c.z + c.w;
@@ -43,19 +42,25 @@ __device__ __forceinline__ void sel_find_bin(const uint32_t* hist, uint32_t kt, 
   const uint32_t a2 = a3 + c.w;
   const uint32_t a1 = a2 + c.z;
   const uint32_t a0 = a1 + c.y;
+  int b = -1;
+  uint32_t ab = 0;
   if (a3 < kt && kt <= a2) {
-    *bin = 4 * l + 3;
-    *above_out = (int)a3;
+    b = 4 * l + 3;
+    ab = a3;
   } else if (a2 < kt && kt <= a1) {
-    *bin = 4 * l + 2;
-    *above_out = (int)a2;
+    b = 4 * l + 2;
+    ab = a2;
   } else if (a1 < kt && kt <= a0) {
-    *bin = 4 * l + 1;
-    *above_out = (int)a1;
+    b = 4 * l + 1;
+    ab = a1;
   } else if (a0 < kt && kt <= a0 + c.x) {
-    *bin = 4 * l;
-    *above_out = (int)a0;
+    b = 4 * l;
+    ab = a0;
   }
+  const uint64_t m = __ballot(b >= 0);
+  const int src = m ? (int)__builtin_ctzll(m) : 0;
+  *bin = m ? __shfl(b, src, kWave) : 0;
+  *above = m ? (int)__shfl(ab, src, kWave) : 0;
 }
 
 // Clears the histograms, the winner count and the winner slots (no barrier).
@@ -86,20 +91,21 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
   const int lane = lane_id();
   const int wave = tid / kWave;
 
-  if (wave == 0) sel_find_bin(sh.hist[0], (uint32_t)k, &sh.bin[0], &sh.above[0]);
-  __syncthreads();
-  const uint32_t hi = (uint32_t)sh.bin[0];
-  const int above_hi = sh.above[0];
+  // Every wave reads the threshold bins off the LDS histograms itself, so
+  // no barrier is needed to broadcast them.
+  int hi_bin = 0, above_hi = 0;
+  sel_find_bin_wave(sh.hist[0], (uint32_t)k, &hi_bin, &above_hi);
+  const uint32_t hi = (uint32_t)hi_bin;
 
   for (long long i = tid; i < n; i += T) {
     const uint32_t key = key_at(i);
     if ((key >> 8) == hi) atomicAdd(&sh.hist[1][key & 255u], 1u);
   }
   __syncthreads();
-  if (wave == 0) sel_find_bin(sh.hist[1], (uint32_t)(k - above_hi), &sh.bin[1], &sh.above[1]);
-  __syncthreads();
-  const uint32_t thr = (hi << 8) | (uint32_t)sh.bin[1];
-  const int take = k - (above_hi + sh.above[1]);  // >= 1 items equal to thr win
+  int lo_bin = 0, above_lo = 0;
+  sel_find_bin_wave(sh.hist[1], (uint32_t)(k - above_hi), &lo_bin, &above_lo);
+  const uint32_t thr = (hi << 8) | (uint32_t)lo_bin;
+  const int take = k - (above_hi + above_lo);  // >= 1 items equal to thr win
   const bool all_ties = (take == (int)sh.hist[1][thr & 255u]);
 
   for (long long i = tid; i < n; i += T) {
@@ -150,7 +156,12 @@ __device__ __forceinline__ void select_topk(KeyAt key_at, long long n, int k, ui
 // Output rank of winner `c` among the k winners in sel (best = 0).
 __device__ __forceinline__ int rank_of(uint64_t c, const uint64_t* sel, int k) {
   int r = 0;
-  for (int m = 0; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
+  int m = 0;
+  for (; m + 8 <= k; m += 8) {  // eight independent LDS reads in flight
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r += (sel[m + u] > c) ? 1 : 0;
+  }
+  for (; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
   return r;
 }
 

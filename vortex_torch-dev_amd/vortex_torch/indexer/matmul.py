@@ -46,11 +46,14 @@ class PendingGemv(_deferred.Pending):
                 if p is mean or p is self:
                     break
                 p.flush()
-        if isinstance(mean, _deferred.PendingMean):
+        # The kernel folds the mean in when its fp32 sum cannot differ from
+        # torch's (at most two query heads per kv head); otherwise torch's
+        # mean runs first and the kernel starts from its result.
+        if isinstance(mean, _deferred.PendingMean) and int(mean.q.shape[1]) <= 2:
             q, x_out = mean.q, mean.out
         else:
             _deferred.materialize(self.x)
-            q, x_out = self.x, None
+            q, x_out, mean = self.x, None, None
         _hip.indexer_fused(
             q, x_out, self.y, self.op.output_buffer,
             ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
