@@ -15,7 +15,19 @@ its 27 per-layer launches); unfused_us_per_step (the same step with every op
 launched separately, VORTEX_FUSE=0); cpu_baseline (the CPU oracle on a
 bounded sample of the same step).
 
+Other configurations (side measurements, not the headline):
+  --config c3 / c5   the same decode step at C3 (8 x 32k tokens, top-64) or C5
+                     (MLA latent cache, D 576, G 16, top-32) shape;
+  --config c4        page-finish burst: CMean + CMax of 65,536 pages (1M loc
+                     entries) into a 70k-page pool, fused (one pass over K)
+                     and as two separate ops.
+  --traffic-probe    launches the fused indexer kernel of every layer eagerly,
+                     then a bf16 negation of a 512 MiB buffer (a copy kernel of
+                     known size), and exits: the program a counter pass
+                     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) profiles.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--config c2|c3|c4|c5] [--layers N] [--traffic-probe]
 """
 from __future__ import annotations
 
@@ -38,6 +50,11 @@ import workloads as W  # noqa: E402
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 HBM_PEAK_GBPS = 8000.0
 
+# HBM bytes per fused-indexer launch from the FETCH_SIZE and WRITE_SIZE
+# counter passes over --traffic-probe (each scaled by what the counter reads
+# for the probe's copy kernel of known size), keyed by (config, layers).
+TRAFFIC_BYTES_PER_LAUNCH: dict = {}
+
 
 def _parse():
     ap = argparse.ArgumentParser()
@@ -48,7 +65,40 @@ def _parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-unfused", action="store_true", help="skip the unfused comparison")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run the kernels a counter pass profiles, print their sizes, exit")
     return ap.parse_args()
+
+
+DECODE_CONFIGS = {
+    "c2": ("C2: decode step, batch 64, L~U[1024,8192], 27 sparse layers, Qwen3-1.7B head shape "
+           "(H_q 16, H_kv 8, D 128), page 16, top-30 + 1 BOS + 1 EOS, 40k-page shared pool, "
+           "per-layer pools; one HIP graph per step"),
+    "c3": ("C3: decode step, batch 8 x 32768 tokens (2048 pages per request), 27 sparse layers, "
+           "H_q 16, H_kv 8, D 128, page 16, top-64 + 1 BOS + 1 EOS; one HIP graph per step"),
+    "c5": ("C5: MLA latent-cache decode step, batch 32, L~U[4096,16384], 27 sparse layers, "
+           "1 latent head, G 16, D 576, page 16, top-32 + 1 BOS + 1 EOS; one HIP graph per step"),
+}
+
+
+def fused_kernel_name(batch: W.DecodeBatch) -> str:
+    """Kernel instance the fused launch selects (VTX_FUSED_AUTO: split layout
+    when there are fewer than two segments per compute unit)."""
+    from vortex_torch._deferred import fused_layout
+
+    lpr, vpl = {64: (8, 1), 128: (16, 1), 256: (16, 2), 512: (16, 4), 576: (8, 9)}[batch.head_dim]
+    segments = batch.batch * batch.num_kv_heads
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    layout = fused_layout()
+    if layout == 2 or (layout == 0 and segments < 2 * cus):
+        small_pass = 32 if batch.head_dim <= 128 else 16
+        mid = max(1, batch.max_pages_per_request - batch.bos - batch.eos)
+        large = segments * -(-mid // (4 * small_pass)) > 4 * cus
+        return f"indexer_split_kernel<256, {lpr}, {vpl}, {small_pass * (2 if large else 1)}>"
+    mp = batch.max_pages_per_request
+    T = 256 if mp <= 256 else (512 if mp <= 1024 else 1024)
+    return f"indexer_fused_kernel<{T}, {lpr}, {vpl}>"
 
 
 class DecodeStep:
@@ -88,6 +138,10 @@ class DecodeStep:
         self.ictx.execute()
         self.cctx.execute()
         self.qmean = torch.empty((B * H, 1, D), device=dev, dtype=torch.bfloat16)
+        self.premeaned = None
+        if G > 2:
+            with torch._C.DisableTorchFunctionSubclass():
+                self.premeaned = [qp.mean(dim=1, keepdim=True) for (_, _, qp) in self.plain]
 
     def run(self):
         from vortex_torch.indexer.utils_sglang import plan_decode
@@ -100,14 +154,20 @@ class DecodeStep:
     def indexer_kernels_only(self):
         """The fused indexer kernel of every layer, launched directly."""
         from vortex_torch import _hip
+        from vortex_torch._deferred import fused_layout
 
         ic, b = self.ictx, self.batch
-        for f, (_, cen, qp) in zip(self.flows, self.plain):
+        for i, (f, (_, cen, qp)) in enumerate(zip(self.flows, self.plain)):
             with torch._C.DisableTorchFunctionSubclass():
-                _hip.indexer_fused(qp, self.qmean, cen, f.gemv.output_buffer, ic.dense_kv_indptr,
+                if self.premeaned is not None:  # G > 2: the step hands the kernel torch's mean
+                    q, x_out = self.premeaned[i], None
+                else:
+                    q, x_out = qp, self.qmean
+                _hip.indexer_fused(q, x_out, cen, f.gemv.output_buffer, ic.dense_kv_indptr,
                                    ic.sparse_kv_indptr, ic.dense_kv_indices, ic.sparse_kv_indices,
                                    b.batch * b.num_kv_heads, b.topk, b.bos, b.eos,
-                                   b.max_pages_per_request)
+                                   b.max_pages_per_request, seg_counters=f.output_func.seg_counters,
+                                   mode=fused_layout())
 
 
 def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: np.ndarray) -> dict:
@@ -124,8 +184,10 @@ def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: n
     # topK: score + row id per candidate page, top-k ids written
     topk = covered * (2 + 4) + sel_segs * batch.topk * 4
     qmean = q_in + q_out
-    # fused kernel: query in, mean out, row ids + centroid rows in, scores out, ids out
-    fused = q_in + q_out + covered * (4 + 2 * D + 2) + sel_segs * batch.topk * 4 + (B * H + 1) * 8
+    # fused kernel: query in (the G heads, or torch's mean when G > 2), mean out
+    # (G <= 2), row ids + centroid rows in, scores out, ids out
+    fused_q = q_in + q_out if G <= 2 else q_out
+    fused = fused_q + covered * (4 + 2 * D + 2) + sel_segs * batch.topk * 4 + (B * H + 1) * 8
     ndense = int(dip[-1])
     plan_b = ndense * 4 + (ndense // H) * 4 + 2 * (B * H + 1) * 4 + int(plan["sparse_indptr"][-1]) * 4 + B * 16
     finishing = int(((loc_host + 1) % P == 0).sum()) * H
@@ -200,39 +262,40 @@ def cpu_baseline(batch: W.DecodeBatch, step: DecodeStep, sample_layers: int = 8)
             t_layers += time.perf_counter() - t0
     per_step = t_plan + t_layers * step.layers / n_layers
     return {"value": round(per_step * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": f"plan + {n_layers} of {step.layers} layers of the same C2 step (oracle, numpy, "
+            "sample": f"plan + {n_layers} of {step.layers} layers of the same step (oracle, numpy, "
                       f"1 thread), layer time scaled to {step.layers} layers; measured "
                       f"{t_plan + t_layers:.2f} s"}
 
 
-def main():
-    args = _parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
-                                   "(the indexer shards by request / kv head with no exchange)"}))
-        sys.exit(2)
-    if not torch.cuda.is_available():
-        print(json.dumps({"error": "no GPU visible"}))
-        sys.exit(2)
-    from vortex_torch import _hip
+def plan_summary(step: DecodeStep) -> dict:
+    """The planner's outputs the byte count needs, read back from the device
+    after the timed region (segment bounds and the workload list)."""
+    ic, b = step.ictx, step.batch
+    S = b.batch * b.num_kv_heads
+    with torch._C.DisableTorchFunctionSubclass():
+        nw = int(ic.winfo_num_workloads[0].item())
+        return {
+            "dense_indptr": ic.dense_kv_indptr[:S + 1].cpu().numpy(),
+            "sparse_indptr": ic.sparse_kv_indptr[:S + 1].cpu().numpy(),
+            "winfo_len": ic.winfo_kv_lens[:nw].cpu().numpy(),
+        }
 
-    _hip.load_library()
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    batch = W.c2()
-    print(f"[bench] building C2 step: {batch.batch} requests, {args.layers} layers", file=sys.stderr, flush=True)
+
+def bench_decode(args, dev) -> dict:
+    batch = getattr(W, args.config)()
+    print(f"[bench] building {args.config.upper()} step: {batch.batch} requests, {args.layers} layers",
+          file=sys.stderr, flush=True)
     step = DecodeStep(batch, args.layers, dev)
 
-    from oracle import vortex_oracle as O  # sizes the algorithmic byte count only
-
-    plan = O.plan_decode(batch.seq_lens.numpy(), batch.req_to_token.numpy(), batch.req_indices.numpy(),
-                         batch.page_size, batch.num_kv_heads, batch.topk, batch.bos, batch.eos, batch.max_chunk)
-    nbytes = algorithmic_bytes(batch, plan, args.layers, step.loc_host)
+    if args.traffic_probe:
+        return traffic_probe(step, dev)
 
     os.environ["VORTEX_FUSE"] = "1"
     g = capture(step.run)
     us_step = time_graph(g, args.steps, args.warmup) * 1000.0
     print(f"[bench] step {us_step:.1f} us", file=sys.stderr, flush=True)
+    plan = plan_summary(step)
+    nbytes = algorithmic_bytes(batch, plan, args.layers, step.loc_host)
 
     gk = capture(step.indexer_kernels_only)
     us_fused = time_graph(gk, args.kernel_reps, 3) * 1000.0 / args.layers
@@ -249,6 +312,7 @@ def main():
         print(f"[bench] unfused step {unfused:.1f} us", file=sys.stderr, flush=True)
 
     gbps = nbytes["step"] / (us_step * 1e-6) / 1e9
+    kernel = fused_kernel_name(batch)
     out = {
         "metric": METRIC,
         "value": round(us_step, 2),
@@ -261,11 +325,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded; random-init K, centroid and query tensors of the C2 shapes)",
+        "data": f"synthetic (seeded; random-init K, centroid and query tensors of the "
+                f"{args.config.upper()} shapes)",
         "config": {
-            "workload": "C2: decode step, batch 64, L~U[1024,8192], 27 sparse layers, Qwen3-1.7B "
-                        "head shape (H_q 16, H_kv 8, D 128), page 16, top-30 + 1 BOS + 1 EOS, "
-                        "40k-page shared pool, per-layer pools; one HIP graph per step",
+            "workload": DECODE_CONFIGS[args.config],
             "batch": batch.batch,
             "layers": args.layers,
             "dense_pages": int(plan["dense_indptr"][-1]),
@@ -277,13 +340,13 @@ def main():
         "algorithmic_bytes_per_step": nbytes["step"],
         "unfused_us_per_step": unfused,
         "roofline": {
-            "kernel": "indexer_fused_kernel<512,16,1> (q-mean + GeMV + top-k, one layer)",
+            "kernel": f"{kernel} (q-mean + GeMV + top-k, one layer)",
             "bound": "hbm",
             "achieved": round(fused_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(fused_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get((args.config, args.layers)),
             "us_per_launch": round(us_fused, 3),
             "bytes_per_launch": nbytes["fused"],
         },
@@ -291,6 +354,117 @@ def main():
     if not args.no_cpu:
         print("[bench] cpu baseline (oracle)", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(batch, step)
+    return out
+
+
+def traffic_probe(step: DecodeStep, dev) -> dict:
+    """Kernels for a counter pass: every layer's fused indexer launch (twice:
+    the second pass is the one to read, the first warms the code object and
+    the TLB like the timed replays), then a copy kernel of known size."""
+    step.run()  # the planner fills the block tables the kernels read
+    with torch._C.DisableTorchFunctionSubclass():
+        for _ in range(2):
+            step.indexer_kernels_only()
+        n = 256 << 20  # bf16 elements: 512 MiB read + 512 MiB written
+        src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    return {"probe": "traffic", "fused_kernel": fused_kernel_name(step.batch), "launches": 2 * step.layers,
+            "copy_kernel": "neg (bf16)", "copy_read_bytes": 2 * n, "copy_write_bytes": 2 * n}
+
+
+def bench_burst(args, dev) -> dict:
+    """C4: CMean + CMax of every page a chunked prefill finished."""
+    from vortex_torch import cache
+    from vortex_torch.abs import FORMAT, as_vtensor
+    from vortex_torch.utils import ReduceType
+
+    case = W.c4()
+    H, P, D = case.num_kv_heads, case.page_size, case.head_dim
+    rows = case.pool_pages * H
+    print(f"[bench] building C4 burst: {case.pages.numel()} pages, {case.loc.numel()} loc entries",
+          file=sys.stderr, flush=True)
+    k = as_vtensor(W.randn_bf16((rows, P, D), 3, dev), FORMAT.PAGED)
+    cmean = as_vtensor(torch.zeros((rows, 1, D), device=dev, dtype=torch.bfloat16), FORMAT.PAGED)
+    cmax = as_vtensor(torch.zeros((rows, 1, D), device=dev, dtype=torch.bfloat16), FORMAT.PAGED)
+    loc = case.loc.to(dev)
+    ctx = cache.Context()
+    ctx.page_size, ctx.total_num_pages, ctx.head_num, ctx.head_dim = P, case.pool_pages, H, D
+    ctx.max_new_tokens_per_batch = int(loc.numel())
+    ctx._created = True
+    mean_op, max_op = cache.Mean(dim=1), cache.Max(dim=1)
+    multi = cache.MultiReduce([ReduceType.Mean, ReduceType.Max], dim=1)
+    ctx.profile()
+    mean_op(k, cmean, loc=loc, ctx=ctx)
+    max_op(k, cmax, loc=loc, ctx=ctx)
+    multi(k, [cmean, cmax], loc=loc, ctx=ctx)
+    ctx.execute()
+
+    def fused():
+        multi(k, [cmean, cmax], loc=loc, ctx=ctx)
+
+    def separate():
+        mean_op(k, cmean, loc=loc, ctx=ctx)
+        max_op(k, cmax, loc=loc, ctx=ctx)
+
+    n_tiles = case.pages.numel() * H
+    k_bytes = n_tiles * P * D * 2
+    fused_bytes = k_bytes + 2 * n_tiles * D * 2 + loc.numel() * 8
+    separate_bytes = 2 * (k_bytes + n_tiles * D * 2 + loc.numel() * 8)
+    us_fused = time_graph(capture(fused), args.steps, args.warmup) * 1000.0
+    us_sep = time_graph(capture(separate), max(5, args.steps // 2), 3) * 1000.0
+    gbps = fused_bytes / (us_fused * 1e-6) / 1e9
+    print(f"[bench] C4 fused {us_fused:.1f} us ({gbps:.0f} GB/s), separate {us_sep:.1f} us",
+          file=sys.stderr, flush=True)
+    need = 1 | 2  # Sum | Max statistics
+    return {
+        "metric": "us per page-finish burst (CMean + CMax) and achieved HBM GB/s",
+        "value": round(us_fused, 2),
+        "unit": "us/burst",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_fused / 1000.0, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded; K ~ N(0,1) bf16, pages and loc order seeded permutations)",
+        "config": {"workload": "C4: page-finish burst, 65,536 pages x 8 heads (1,048,576 loc entries) "
+                               "of a 70k-page pool, D 128, page 16, CMean + CMax bf16 outputs",
+                   "pages": int(case.pages.numel()), "loc_entries": int(loc.numel())},
+        "achieved_GBps": round(gbps, 1),
+        "separate_ops_us": round(us_sep, 2),
+        "separate_ops_GBps": round(separate_bytes / (us_sep * 1e-6) / 1e9, 1),
+        "roofline": {
+            "kernel": f"reduce_rows_vec_kernel<16, {need}> (CMean + CMax, one pass over K)",
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "bytes_per_launch": fused_bytes,
+        },
+    }
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
+                                   "(the indexer shards by request / kv head with no exchange)"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(2)
+    from vortex_torch import _hip
+
+    _hip.load_library()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    out = bench_burst(args, dev) if args.config == "c4" else bench_decode(args, dev)
     print(json.dumps(out), flush=True)
 
 

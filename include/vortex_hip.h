@@ -126,10 +126,15 @@ int vtx_topk_select(const uint16_t* score, int64_t score_len,
                     int32_t reserved_bos, int32_t reserved_eos,
                     int32_t max_num_pages, void* stream);
 
+/* Work layouts of vtx_indexer_fused. */
+#define VTX_FUSED_AUTO 0     /* the library chooses */
+#define VTX_FUSED_SEGMENT 1  /* one workgroup per segment */
+#define VTX_FUSED_SPLIT 2    /* a segment's pages over several workgroups */
+
 /*
  * Fused indexer step of one sparse layer: query head-group mean, GeMV over
- * every segment's middle pages, top-k select — one launch, one workgroup per
- * segment.  No single counterpart in the reference: it is the composition of
+ * every segment's middle pages, top-k select — one launch.  No single
+ * counterpart in the reference: it is the composition of
  * `q.mean(dim=1, keepdim=True)` (vortex_torch/flow/algorithms.py:168), GeMV
  * (mv_bpr, indexer/triton_kernels/mv_impl.py:6-81) over the planner's
  * workload list and topK (csrc/topk.cu:56-203), for a block table built by
@@ -142,6 +147,15 @@ int vtx_topk_select(const uint16_t* score, int64_t score_len,
  *   sparse_kv_indices[sparse_kv_indptr[s] + bos + i] = i-th best of them.
  * With group_size == 0 the query rows are taken from x [S, D] instead.
  * q: bf16 [q_rows, group_size, head_dim]; y: bf16 [y_rows, head_dim].
+ *
+ * seg_counters (optional, int32, at least eff_batch_size entries, all zero
+ * before the first call) lets the library split long segments over several
+ * workgroups: the last workgroup of a segment to finish selects its top-k
+ * and sets the segment's counter back to zero.  Calls that share one
+ * counter buffer must be ordered on one stream.  mode: VTX_FUSED_AUTO
+ * (split when there are fewer than two segments per compute unit and the
+ * counters are given), VTX_FUSED_SEGMENT or VTX_FUSED_SPLIT.  Outputs are
+ * identical in every mode.
  */
 int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                       const uint16_t* x, uint16_t* x_out, const uint16_t* y,
@@ -151,6 +165,7 @@ int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                       int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                       int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                       int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
+                      int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
                       void* stream);
 
 /* 1 if vtx_indexer_fused handles this head_dim (64, 128, 256, 512, 576). */

@@ -94,10 +94,18 @@ def test_kernels_reproduce_fixture(gpu):
     cov = G["gemv_covered"]
     got = O.bf16_to_f32(sc.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
     np.testing.assert_allclose(got[cov], O.bf16_to_f32(G["gemv"])[cov], rtol=1e-2, atol=1e-3)
-    sc2 = torch.zeros_like(sc)
-    qm2 = torch.empty_like(qm)
-    sp2 = torch.full_like(sparse, -1)
-    _hip.indexer_fused(q, qm2, cen, sc2, dptr, sptr, dense, sp2, 8, TOPK, BOS, EOS, 256)
-    assert torch.equal(qm2, qm)
-    got2 = O.bf16_to_f32(sc2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
-    np.testing.assert_allclose(got2[cov], O.bf16_to_f32(G["gemv"])[cov], rtol=1e-2, atol=1e-3)
+    for mode in (_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT):
+        sc2 = torch.zeros_like(sc)
+        qm2 = torch.empty_like(qm)
+        sp2 = torch.full_like(sparse, -1)
+        counters = torch.zeros(8, dtype=torch.int32, device=dev)
+        _hip.indexer_fused(q, qm2, cen, sc2, dptr, sptr, dense, sp2, 8, TOPK, BOS, EOS, 256,
+                           seg_counters=counters, mode=mode)
+        assert torch.equal(qm2, qm)
+        got2 = O.bf16_to_f32(sc2.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1))
+        np.testing.assert_allclose(got2[cov], O.bf16_to_f32(G["gemv"])[cov], rtol=1e-2, atol=1e-3)
+        # its selection is the top-k kernel's selection on its own scores
+        sp3 = torch.full_like(sparse, -1)
+        _hip.topk_select(sc2, dptr, sptr, dense, sp3, 8, TOPK, BOS, EOS, 256)
+        assert torch.equal(sp2, sp3)
+        assert int(counters.abs().sum()) == 0

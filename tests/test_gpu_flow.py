@@ -32,8 +32,9 @@ def _plan(batch, ic, dev):
     plan_decode(b.seq_lens, b.req_to_token, b.req_indices, ic)
 
 
+@pytest.mark.parametrize("mode", [_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT])
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
-def test_fused_kernel_matches_separate_kernels(gpu, name):
+def test_fused_kernel_matches_separate_kernels(gpu, name, mode):
     dev = gpu
     batch = getattr(W, name)()
     ic, _ = W.make_contexts(batch, dev)
@@ -53,13 +54,17 @@ def test_fused_kernel_matches_separate_kernels(gpu, name):
     _hip.topk_select(sc_ref, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp_ref,
                      S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
 
-    # fused
-    qm = torch.empty_like(qm_ref)
-    sc = torch.full_like(sc_ref, -5.0)
-    sp = ic.sparse_kv_indices.clone()
-    _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp,
-                       S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
-    torch.cuda.synchronize()
+    # fused, twice with the same counters (the first call must leave them zeroed)
+    counters = torch.zeros(S, dtype=torch.int32, device=dev)
+    for _ in range(2):
+        qm = torch.empty_like(qm_ref)
+        sc = torch.full_like(sc_ref, -5.0)
+        sp = ic.sparse_kv_indices.clone()
+        _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp,
+                           S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request,
+                           seg_counters=counters, mode=mode)
+        torch.cuda.synchronize()
+        assert int(counters.abs().sum()) == 0, "segment counters not reset"
     if G <= 2:
         assert torch.equal(qm, qm_ref), "q-mean differs from torch.mean"
     else:  # the fp32 sum of G > 2 heads may round differently in another order
@@ -75,7 +80,8 @@ def test_fused_kernel_matches_separate_kernels(gpu, name):
     np.testing.assert_array_equal(_np(sp), exp)
 
 
-def test_fused_kernel_extra_query_rows(gpu):
+@pytest.mark.parametrize("mode", [_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT])
+def test_fused_kernel_extra_query_rows(gpu, mode):
     # more query rows than segments (padded batch): every row gets its mean
     dev = gpu
     batch = W.c1()
@@ -86,8 +92,10 @@ def test_fused_kernel_extra_query_rows(gpu):
     y = W.randn_bf16((batch.pool_pages * batch.num_kv_heads, 1, 128), 4, dev)
     qm = torch.empty((S + 5, 1, 128), device=dev, dtype=torch.bfloat16)
     sc = torch.zeros((ic.dense_kv_indices.numel(), 1, 1), device=dev, dtype=torch.bfloat16)
+    counters = torch.zeros(S, dtype=torch.int32, device=dev)
     _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices,
-                       ic.sparse_kv_indices, S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+                       ic.sparse_kv_indices, S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request,
+                       seg_counters=counters, mode=mode)
     assert torch.equal(qm, q.mean(dim=1, keepdim=True))
 
 
@@ -172,8 +180,10 @@ def test_flow_end_to_end_against_oracle(gpu):
     np.testing.assert_array_equal(_np(run.ic.sparse_kv_indices), sel)
 
 
-def test_flow_graph_replay(gpu):
-    batch = W.c2()
+@pytest.mark.parametrize("name", ["c2", "c3"])
+def test_flow_graph_replay(gpu, name):
+    # C2 runs one workgroup per segment, C3 (64 segments) the split layout
+    batch = getattr(W, name)()
     run = _FlowRun(batch, gpu, seed=9)
     stream = torch.cuda.Stream(gpu)
     stream.wait_stream(torch.cuda.current_stream(gpu))
@@ -199,6 +209,7 @@ def test_flow_graph_replay(gpu):
             assert torch.equal(run.ic.sparse_kv_indices, eager_o), f"replay {rep}: selection differs"
             s = run.flow.gemv.output_buffer
             assert torch.equal(s[s != 0.5], eager_s[s != 0.5])
+            assert int(run.flow.output_func.seg_counters.abs().sum()) == 0
 
 
 def test_deferred_mean_materializes_on_use(gpu):

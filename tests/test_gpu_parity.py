@@ -294,3 +294,46 @@ def test_reduce_negative_and_out_of_range_loc(gpu):
     # C semantics: loc = -1 closes "page 0"; rows beyond the pool are skipped
     loc = [-1, 15, 16 * 49 + 15, 16 * 1000 + 15]
     reduce_case(gpu, 50, 2, 16, 128, loc, O.MAX)
+
+
+def test_reduce_c4_burst_full_size(gpu):
+    """C4 at full size: 65,536 pages (1,048,576 loc entries) of a 70k-page pool,
+    CMean + CMax in one pass.  CMax must equal torch.amax of the same tiles
+    bit for bit, CMean torch's fp32 mean within tolerance; rows of pages that
+    did not close keep their contents; an fp32 CMean output holds the same
+    bf16-rounded values.  A sample of pages is also checked against the oracle."""
+    dev = gpu
+    case = W.c4()
+    H, P, D = case.num_kv_heads, case.page_size, case.head_dim
+    x = W.randn_bf16((case.pool_pages * H, P, D), 3, dev)
+    loc = case.loc.to(dev)
+    cm = torch.full((case.pool_pages * H, 1, D), 7.0, device=dev, dtype=torch.bfloat16)
+    cx = torch.full_like(cm, 7.0)
+    _hip.page_reduce_multi(x, [cm, cx], [O.MEAN, O.MAX], loc, H, P, 1)
+    cm32 = torch.full(cm.shape, 7.0, device=dev, dtype=torch.float32)
+    _hip.page_reduce(x, cm32, loc, H, P, 1, O.MEAN)
+
+    rows = (case.pages.to(dev)[:, None] * H + torch.arange(H, device=dev)[None, :]).reshape(-1)
+    tiles = x[rows]
+    assert torch.equal(cx[rows], tiles.amax(dim=1, keepdim=True)), "CMax differs from torch.amax"
+    exp_mean = tiles.float().mean(dim=1, keepdim=True)
+    del tiles
+    torch.testing.assert_close(cm[rows].float(), exp_mean, rtol=RTOL, atol=ATOL)
+    assert torch.equal(cm32[rows], cm[rows].float()), "fp32 CMean output is not the bf16-rounded mean"
+    closed = torch.zeros(case.pool_pages * H, dtype=torch.bool, device=dev)
+    closed[rows] = True
+    for out in (cm, cx, cm32):
+        assert bool((out[~closed] == 7.0).all()), "a row of an unfinished page was written"
+
+    # oracle on a sample of 64 pages, through a compact copy of their tiles
+    sample = case.pages[:64]
+    srows = (sample[:, None] * H + torch.arange(H)[None, :]).reshape(-1)
+    xs = _bits(x[srows.to(dev)]).reshape(len(srows), P, D)
+    sloc = np.arange(len(sample)) * P + (P - 1)
+    for out, rtype in ((cm, O.MEAN), (cx, O.MAX)):
+        exp, _ = O.page_reduce(xs, np.zeros((len(srows), 1, D), np.uint16), sloc, H, P, 1, rtype)
+        got = _bits(out[srows.to(dev)]).reshape(len(srows), 1, D)
+        if rtype == O.MAX:
+            np.testing.assert_array_equal(got, exp)
+        else:
+            np.testing.assert_allclose(O.bf16_to_f32(got), O.bf16_to_f32(exp), rtol=RTOL, atol=ATOL)

@@ -125,6 +125,29 @@ def c5(seed: int = 4) -> DecodeBatch:
                       head_dim=576, topk=32, bos=1, eos=1, row_tokens=16384)
 
 
+@dataclass
+class BurstCase:
+    """A page-finish burst: every slot of `pages` appears in loc (shuffled)."""
+
+    loc: torch.Tensor    # int64 [pages * page_size]
+    pages: torch.Tensor  # int64 [n] physical pages that close
+    pool_pages: int
+    page_size: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 128
+
+
+def c4(seed: int = 3, pool_pages: int = 70000, n_pages: int = 65536) -> BurstCase:
+    """C4: 65,536 pages of a 70k-page pool finish at once (after a chunked
+    prefill); loc lists all 16 slots of each, in shuffled order."""
+    g = torch.Generator().manual_seed(seed)
+    pages = torch.randperm(pool_pages, generator=g)[:n_pages]
+    P = 16
+    slots = (pages[:, None] * P + torch.arange(P)[None, :]).reshape(-1)
+    loc = slots[torch.randperm(slots.numel(), generator=g)]
+    return BurstCase(loc=loc.to(torch.int64), pages=pages.to(torch.int64), pool_pages=pool_pages, page_size=P)
+
+
 def random_small(seed: int) -> DecodeBatch:
     """Small random layout with edge cases (empty requests, exact page
     multiples, segments shorter than the budget, bos/eos 0)."""

@@ -55,11 +55,11 @@ struct FusedArgs {
 
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
 // fp32 mean of its G rows (torch's mean), or the row itself when G == 0.
-// Lane group 0 of wave 0 also stores the mean to x_out.
+// Lanes with `store` set (one lane group per row) also write the mean to x_out.
 template <int LPR, int VPL, int kQRegs>
 __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv)[kQRegs][VPL],
-                                          bool q_in_regs, const uint16_t* qb, int seg, int wave,
-                                          int grp, int col, float (&xs)[VPL][8]) {
+                                          bool q_in_regs, const uint16_t* qb, int seg, bool store,
+                                          int col, float (&xs)[VPL][8]) {
   const int D = a.dim;
   if (a.G > 0) {
 #pragma unroll
@@ -96,7 +96,7 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
         mb[v][e] = vtx::f32_to_bf16(xs[v][e] * a.inv_g);
         xs[v][e] = vtx::bf16_to_f32(mb[v][e]);
       }
-    if (a.x_out && wave == 0 && grp == 0) {
+    if (store && a.x_out) {
       uint16_t* xo = a.x_out + (long long)seg * D;
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
@@ -120,15 +120,81 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
   }
 }
 
+// One wave pass over `cnt` <= kPass consecutive pages of a segment; lane l
+// (< cnt) holds the l-th page's centroid row id in my_row.  A row is split over
+// LPR lanes x VPL 16-byte vectors (kRowsPerLoad = 64 / LPR rows per wave-wide
+// load, kSlots = kPass / kRowsPerLoad rows per lane), every lane issues its
+// row loads before any arithmetic, and a reduce-scatter over the LPR lanes
+// leaves each finished score on one lane.  Returns that score (fp32) and its
+// position in the pass in *r; *r = -1 on lanes that own no page.
+template <int LPR, int VPL, int kPass>
+__device__ __forceinline__ float score_pass(const FusedArgs& a, int my_row, int cnt,
+                                            const float (&xs)[VPL][8], int grp, int col, int* r) {
+  constexpr int kRowsPerLoad = vtx::kWave / LPR;
+  constexpr int kSlots = kPass / kRowsPerLoad;
+  constexpr int kBatch = VPL <= 2 ? kSlots : (kSlots < 2 ? kSlots : 2);  // slots loaded together
+  static_assert(kSlots >= 1 && kSlots <= LPR && kSlots * kRowsPerLoad == kPass, "pass geometry");
+  const int D = a.dim;
+  int first = __shfl(my_row, 0, vtx::kWave);
+  if (first < 0 || first >= a.y_rows) first = 0;
+  float acc[kSlots];
+#pragma unroll
+  for (int i0 = 0; i0 < kSlots; i0 += kBatch) {
+    vtx::U4 buf[kBatch][VPL];
+    bool live[kBatch];
+#pragma unroll
+    for (int ii = 0; ii < kBatch; ++ii) {
+      const int row = __shfl(my_row, (i0 + ii) * kRowsPerLoad + grp, vtx::kWave);
+      live[ii] = row >= 0 && row < a.y_rows;
+      if ((i0 + ii) * kRowsPerLoad < cnt) {  // wave-uniform: slots past the pass are skipped
+        const uint16_t* yr = a.y + (long long)(live[ii] ? row : first) * D;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16(yr + (v * LPR + col) * 8);
+      } else {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::U4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int ii = 0; ii < kBatch; ++ii) {
+      const float s = vtx::dot_row<VPL>(buf[ii], xs);
+      acc[i0 + ii] = live[ii] ? s : 0.f;
+    }
+  }
+  // Reduce-scatter over the slots (lane keeps slot bits of col from the top),
+  // then fold the lanes that still share a slot.  The strides run LPR/2 down
+  // to 1 in both parts: the same summation tree as gemv.hip.
+#pragma unroll
+  for (int half = kSlots / 2, stride = LPR / 2; half >= 1; half >>= 1, stride >>= 1) {
+    const bool upper = (col & stride) != 0;
+#pragma unroll
+    for (int t = 0; t < half; ++t) {
+      const float send = upper ? acc[t] : acc[t + half];
+      const float keep = upper ? acc[t + half] : acc[t];
+      acc[t] = keep + __shfl_xor(send, stride, vtx::kWave);
+    }
+  }
+  constexpr int kShare = LPR / kSlots;  // lanes holding the same slot
+#pragma unroll
+  for (int d = kShare / 2; d >= 1; d >>= 1) acc[0] += __shfl_xor(acc[0], d, vtx::kWave);
+  const int pos = (col / kShare) * kRowsPerLoad + grp;
+  *r = ((col % kShare) == 0 && pos < cnt) ? pos : -1;
+  return acc[0];
+}
+
+// Pages per wave pass: 64 when a row is one 16-byte vector per lane, else 32.
+template <int VPL>
+constexpr int segment_pass() {
+  return VPL == 1 ? 64 : 32;
+}
+
+// One workgroup per segment: scores into LDS, select in LDS.
 template <int T, int LPR, int VPL>
 __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
-  constexpr int kPass = VPL == 1 ? 64 : 32;        // at most this many pages per wave pass
-  constexpr int kSlots = kPass / kRowsPerLoad;     // pages per lane per pass
-  constexpr int kBatch = VPL <= 2 ? kSlots : 2;    // slots loaded together
-  constexpr int kQRegs = VPL <= 2 ? 2 : 1;         // query rows prefetched
-  static_assert(kSlots >= 1 && kSlots <= LPR, "pass geometry");
+  constexpr int kPass = segment_pass<VPL>();
+  constexpr int kQRegs = VPL <= 2 ? 2 : 1;  // query rows prefetched
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
 
@@ -140,6 +206,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int col = lane % LPR;
   const int k = a.topk;
   const int D = a.dim;
+  const bool store_mean = wave == 0 && grp == 0;
 
   // ---- 1. query rows (issued first: only needed once centroid rows arrive)
   vtx::U4 qv[kQRegs][VPL];
@@ -174,7 +241,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // evaluated after the first row ids are requested so the waits overlap
   float xs[VPL][8];
   if (!active) {  // uniform over the workgroup
-    if (a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, wave, grp, col, xs);
+    if (a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
     return;
   }
   vtx::select_init<T>(sel, k, sh);
@@ -190,59 +257,17 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   if (share > kPass) share = kPass;
   for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
     const int cnt = (int)min(share, n - p0);
-    // one coalesced load of the pass's row ids (lane l holds position l),
-    // handed to the lanes that need them with shuffles
+    // one coalesced load of the pass's row ids (lane l holds position l)
     const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
     if (!have_mean) {
-      query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, wave, grp, col, xs);
+      query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
       have_mean = true;
     }
-    int first = __shfl(my_row, 0, vtx::kWave);
-    if (first < 0 || first >= a.y_rows) first = 0;
-    float acc[kSlots];
-#pragma unroll
-    for (int i0 = 0; i0 < kSlots; i0 += kBatch) {
-      vtx::U4 buf[kBatch][VPL];
-      bool live[kBatch];
-#pragma unroll
-      for (int ii = 0; ii < kBatch; ++ii) {
-        const int row = __shfl(my_row, (i0 + ii) * kRowsPerLoad + grp, vtx::kWave);
-        live[ii] = row >= 0 && row < a.y_rows;
-        if ((i0 + ii) * kRowsPerLoad < cnt) {  // wave-uniform: slots past the share are skipped
-          const uint16_t* yr = a.y + (long long)(live[ii] ? row : first) * D;
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16(yr + (v * LPR + col) * 8);
-        } else {
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::U4{0u, 0u, 0u, 0u};
-        }
-      }
-#pragma unroll
-      for (int ii = 0; ii < kBatch; ++ii) {
-        const float s = vtx::dot_row<VPL>(buf[ii], xs);
-        acc[i0 + ii] = live[ii] ? s : 0.f;
-      }
-    }
-    // Reduce-scatter over the slots (lane keeps slot bits of col from the
-    // top), then fold the lanes that still share a slot.
-#pragma unroll
-    for (int half = kSlots / 2, stride = LPR / 2; half >= 1; half >>= 1, stride >>= 1) {
-      const bool upper = (col & stride) != 0;
-#pragma unroll
-      for (int t = 0; t < half; ++t) {
-        const float send = upper ? acc[t] : acc[t + half];
-        const float keep = upper ? acc[t + half] : acc[t];
-        acc[t] = keep + __shfl_xor(send, stride, vtx::kWave);
-      }
-    }
-    constexpr int kShare = LPR / kSlots;  // lanes holding the same slot
-#pragma unroll
-    for (int d = 1; d < kShare; d <<= 1) acc[0] += __shfl_xor(acc[0], d, vtx::kWave);
-    const int slot = col / kShare;
-    const int r = slot * kRowsPerLoad + grp;
-    const int my_rid = __shfl(my_row, r, vtx::kWave);  // row id of this lane's page
-    if ((col % kShare) == 0 && r < cnt) {
-      const uint32_t sb = vtx::f32_to_bf16(acc[0]);
+    int r;
+    const float sc = score_pass<LPR, VPL, kPass>(a, my_row, cnt, xs, grp, col, &r);
+    const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
+    if (r >= 0) {
+      const uint32_t sb = vtx::f32_to_bf16(sc);
       const uint32_t key = vtx::score_key(sb);
       a.score[start + p0 + r] = (uint16_t)sb;
       if (cached) {
@@ -261,14 +286,161 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     const uint16_t* sc = a.score + start;  // this workgroup's own stores
     vtx::select_topk_counted<T>([&](long long i) { return vtx::score_key(sc[i]); }, n, k, sel, sh);
   }
-  for (int j = tid; j < k; j += T) {
-    const uint64_t c = sel[j];
-    const long long pos = vtx::sel_position(c);
-    if (pos < n) a.sidx[obase + vtx::rank_of(c, sel, k)] = cached ? rows[pos] : dseg[pos];
-  }
+  vtx::select_emit<T>(sel, k, n, [&](int r, long long pos) { a.sidx[obase + r] = cached ? rows[pos] : dseg[pos]; });
 }
 
-constexpr int kLdsBudget = 60 * 1024;
+// Stores / loads performed at device scope (every XCD sees them once the
+// store has completed; no copy in a non-coherent cache is used).
+__device__ __forceinline__ void store_coherent(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint16_t load_coherent(const uint16_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split segments: a segment's middle pages are dealt, kChunk = kWaves * kPass
+// at a time, to `cps` workgroups (chunk c takes chunks c, c + cps, ...).  Each
+// workgroup scores its pages and stores the scores; the one that finishes
+// last (per-segment arrival counter in `counters`) selects the top-k from the
+// stored scores.  Nothing waits on another workgroup, so every workgroup runs
+// to completion whatever the others do.  The last one resets the counter to
+// zero for the next launch.
+//
+// Work ids are laid out XCD by XCD (workgroup b runs on XCD b % 8), so the
+// chunks of one segment usually share an L2 and the selecting workgroup reads
+// the other chunks' scores from it.
+template <int T, int LPR, int VPL, int kPass>
+__global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* counters, int32_t cps) {
+  constexpr int kWaves = T / vtx::kWave;
+  constexpr int kRowsPerLoad = vtx::kWave / LPR;
+  constexpr int kChunk = kWaves * kPass;
+  constexpr int kQRegs = VPL <= 2 ? 2 : 1;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ vtx::SelectShared<T> sh;
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = vtx::lane_id();
+  const int wave = tid / vtx::kWave;
+  const int grp = lane / LPR;
+  const int col = lane % LPR;
+  const int k = a.topk;
+  const int D = a.dim;
+
+  const long long per_xcd = gridDim.x / 8;  // the host rounds the grid to a multiple of 8
+  const long long w = (long long)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const long long chunk_items = (long long)a.segments * cps;
+  float xs[VPL][8];
+  vtx::U4 qv[kQRegs][VPL];
+  if (w >= chunk_items) {  // query rows past the segments: only their mean
+    const long long row = a.segments + (w - chunk_items);
+    if (a.x_out && a.G > 0 && row < a.q_rows)
+      query_row<LPR, VPL, kQRegs>(a, qv, false, a.q + row * a.G * D, (int)row, wave == 0 && grp == 0,
+                                  col, xs);
+    return;
+  }
+  const int seg = (int)(w / cps);
+  const int c = (int)(w % cps);
+  const bool store_mean = c == 0 && wave == 0 && grp == 0;
+
+  const bool q_in_regs = a.G > 0 && a.G <= kQRegs;
+  const uint16_t* qb = a.G > 0 ? a.q + (long long)seg * a.G * D : a.x + (long long)seg * D;
+  if (q_in_regs) {
+#pragma unroll
+    for (int g = 0; g < kQRegs; ++g)
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        qv[g][v] = g < a.G ? vtx::ld16(qb + (long long)g * D + (v * LPR + col) * 8) : vtx::U4{0u, 0u, 0u, 0u};
+  }
+
+  const long long start = (long long)a.dindptr[seg] + a.bos;
+  const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
+  const long long obase = (long long)a.sindptr[seg] + a.bos;
+  bool active = k > 0 && n > k;
+  if (active && (start < 0 || start + n > a.score_len || start + n > a.didx_len || obase < 0 ||
+                 obase + k > a.sidx_len))
+    active = false;
+  const long long nchunks = active ? (n + kChunk - 1) / kChunk : 0;
+  const int workers = (int)min(nchunks, (long long)cps);  // workgroups that take part
+  if (c >= workers) {  // nothing to score (or an inactive segment): only the mean
+    if (c == 0 && a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+    return;
+  }
+
+  // ---- scores of this workgroup's chunks
+  const int32_t* dseg = a.didx + start;
+  bool have_mean = false;
+  for (long long ch = c; ch < nchunks; ch += cps) {
+    const long long c0 = ch * kChunk;
+    const long long cn = min((long long)kChunk, n - c0);
+    long long share = (cn + kWaves - 1) / kWaves;
+    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+    const long long p0 = c0 + (long long)wave * share;
+    if (p0 >= c0 + cn) continue;  // wave-uniform
+    const int cnt = (int)min(share, c0 + cn - p0);
+    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
+    if (!have_mean) {
+      query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+      have_mean = true;
+    }
+    int r;
+    const float sc = score_pass<LPR, VPL, kPass>(a, my_row, cnt, xs, grp, col, &r);
+    if (r >= 0) store_coherent(a.score + start + p0 + r, (uint16_t)vtx::f32_to_bf16(sc));
+  }
+  // (wave 0 of chunk 0 always has pages, so the mean has been stored)
+
+  // ---- arrival: the last of the `workers` workgroups selects.  The scores
+  // went out as device-coherent stores; each wave waits until its own have
+  // completed, so they are visible to every XCD before the count moves.  No
+  // cache-wide write-back or invalidate is needed on either side.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(&counters[seg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = old == workers - 1;
+    if (last) __hip_atomic_store(&counters[seg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // ---- top-k of the segment from the stored scores (device-coherent loads)
+  uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
+  uint16_t* keys = reinterpret_cast<uint16_t*>(smem + (size_t)k * sizeof(uint64_t));
+  const bool cached = n <= a.row_cap;
+  const uint16_t* scs = a.score + start;
+  vtx::select_init<T>(sel, k, sh);
+  __syncthreads();
+  // kU loads per thread in flight before any is used
+  constexpr int kU = 8;
+  for (long long base = 0; base < n; base += (long long)T * kU) {
+    uint16_t v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const long long i = base + (long long)u * T + tid;
+      v[u] = i < n ? load_coherent(scs + i) : (uint16_t)0;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const long long i = base + (long long)u * T + tid;
+      if (i < n) {
+        const uint32_t key = vtx::score_key(v[u]);
+        if (cached) keys[i] = (uint16_t)key;
+        vtx::select_count<T>(key, sh);
+      }
+    }
+  }
+  __syncthreads();
+  if (cached) {
+    vtx::select_topk_counted<T>([&](long long i) { return (uint32_t)keys[i]; }, n, k, sel, sh);
+  } else {
+    vtx::select_topk_counted<T>([&](long long i) { return vtx::score_key(load_coherent(scs + i)); }, n, k,
+                                sel, sh);
+  }
+  vtx::select_emit<T>(sel, k, n, [&](int r, long long pos) { a.sidx[obase + r] = dseg[pos]; });
+}
+
+constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS; the select tables take up to ~6 KB more
 constexpr int kMaxTopk = 4096;
 
 template <int T>
@@ -282,6 +454,33 @@ int launch_dim(const FusedArgs& a, int blocks, size_t lds, hipStream_t s) {
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_fused");
+}
+
+constexpr int kSplitThreads = 256;
+
+// Pages per wave pass of the split layout (small chunks; large ones are
+// twice this) and pages per split workgroup.
+int split_pass(int dim) { return dim <= 128 ? 32 : 16; }
+int split_chunk(int dim, bool large) { return (kSplitThreads / 64) * split_pass(dim) * (large ? 2 : 1); }
+
+template <int P>
+int launch_split_pass(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s) {
+  constexpr int T = kSplitThreads;
+  switch (a.dim) {
+    case 64: indexer_split_kernel<T, 8, 1, 2 * P><<<blocks, T, lds, s>>>(a, counters, cps); break;
+    case 128: indexer_split_kernel<T, 16, 1, 2 * P><<<blocks, T, lds, s>>>(a, counters, cps); break;
+    case 256: indexer_split_kernel<T, 16, 2, P><<<blocks, T, lds, s>>>(a, counters, cps); break;
+    case 512: indexer_split_kernel<T, 16, 4, P><<<blocks, T, lds, s>>>(a, counters, cps); break;
+    case 576: indexer_split_kernel<T, 8, 9, P><<<blocks, T, lds, s>>>(a, counters, cps); break;
+    default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
+  }
+  return vtx::check_launch("indexer_fused (split)");
+}
+
+int launch_split(const FusedArgs& a, int32_t* counters, int cps, bool large, int blocks, size_t lds,
+                 hipStream_t s) {
+  return large ? launch_split_pass<32>(a, counters, cps, blocks, lds, s)
+               : launch_split_pass<16>(a, counters, cps, blocks, lds, s);
 }
 
 }  // namespace
@@ -298,6 +497,7 @@ extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t grou
                                  int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                                  int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                                  int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
+                                 int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
                                  void* stream) {
   vtx::clear_error();
   if (eff_batch_size < 0 || group_size < 0 || reserved_bos < 0 || reserved_eos < 0)
@@ -338,23 +538,62 @@ extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t grou
   a.bos = reserved_bos;
   a.eos = reserved_eos;
   a.dim = head_dim;
+  a.row_cap = 0;
 
-  long long want = max_num_pages > 0 ? max_num_pages : 0;
+  if (mode < VTX_FUSED_AUTO || mode > VTX_FUSED_SPLIT)
+    return vtx::fail(VTX_E_INVALID, "indexer_fused: unknown mode %d", mode);
+  const bool have_counters = seg_counters && seg_counters_len >= eff_batch_size;
+  if (mode == VTX_FUSED_SPLIT && !have_counters)
+    return vtx::fail(VTX_E_INVALID, "indexer_fused: split mode needs %d segment counters, got %lld",
+                     eff_batch_size, (long long)(seg_counters ? seg_counters_len : 0));
+  a.segments = eff_batch_size;
+  const long long want = max_num_pages > 0 ? max_num_pages : 0;
+  hipStream_t s = vtx::as_stream(stream);
+  const int cus = vtx::device_cu_count();
+  if (cus <= 0) return vtx::fail(VTX_E_DEVICE, "indexer_fused: cannot query the compute unit count");
+
+  // One workgroup per segment fills the chip when there are at least two
+  // segments per CU; fewer (long contexts, MLA's single latent head) leave
+  // CUs idle, so their pages are split over several workgroups.
+  const bool split = mode == VTX_FUSED_SPLIT ||
+                     (mode == VTX_FUSED_AUTO && have_counters && (long long)eff_batch_size < 2LL * cus);
+  if (split) {
+    // Small chunks when every segment's chunks fit on the chip at once
+    // (four split workgroups per CU), else twice as large; past that,
+    // workgroups loop over several chunks.
+    const long long mid = want - reserved_bos - reserved_eos > 1 ? want - reserved_bos - reserved_eos : 1;
+    const long long resident = 4LL * cus;
+    const long long small = split_chunk(head_dim, false);
+    const bool large = (long long)eff_batch_size * ((mid + small - 1) / small) > resident;
+    const int chunk = split_chunk(head_dim, large);
+    long long cps = (mid + chunk - 1) / chunk;
+    const long long fill = eff_batch_size > 0 ? resident / eff_batch_size : 1;
+    if (cps > fill) cps = fill;
+    if (cps < 1) cps = 1;
+    const long long room = (kLdsBudget - (long long)a.topk * 8) / 2;
+    long long cap = want < room ? want : room;
+    cap &= ~7LL;
+    if (cap < 0) cap = 0;
+    a.row_cap = (int32_t)cap;
+    const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 2;
+    long long items = (long long)eff_batch_size * cps + (a.x_out ? q_rows - eff_batch_size : 0);
+    items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
+    if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
+    if (items == 0) return VTX_OK;
+    return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s);
+  }
+
   const long long room = (kLdsBudget - (long long)a.topk * 8) / 6;
   long long cap = want < room ? want : room;
   cap &= ~7LL;
   if (cap < 0) cap = 0;
   a.row_cap = (int32_t)cap;
   const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 6;
-
-  a.segments = eff_batch_size;
   // With a q_mean output every query row gets a workgroup (rows past the
   // segments only write their mean).
   const long long grid = a.x_out ? q_rows : eff_batch_size;
   if (grid > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many query rows");
   if (grid == 0) return VTX_OK;
-
-  hipStream_t s = vtx::as_stream(stream);
   if (max_num_pages <= 256) return launch_dim<256>(a, (int)grid, lds, s);
   if (max_num_pages <= 1024) return launch_dim<512>(a, (int)grid, lds, s);
   return launch_dim<1024>(a, (int)grid, lds, s);

@@ -15,6 +15,8 @@
 //     bf16 is split over C/8 lanes with one 16-byte load each, the remaining
 //     lanes take further rows, every lane accumulates fp32 over its rows and
 //     a shuffle tree folds the row groups together;
+//   * widths whose 16-byte column count does not divide 64 (D = 576) give
+//     each lane one column vector and load 8 rows of it at a time;
 //   * one pass over the tile feeds up to four outputs (the fused entry point),
 //     so CMean + CMax read K once.
 #include "vtx_device.h"
@@ -185,6 +187,65 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_vec_kernel(ReduceArgs a)
   }
 }
 
+// dim 1, C = 8 * nv for any nv (e.g. 576 = 8 * 72): lane = one 16-byte
+// column vector; a wave covers 64 column vectors of a tile per round and each
+// lane loads its vector from 8 rows at a time before accumulating them.
+template <int NEED>
+__global__ __launch_bounds__(kThreads) void reduce_colvec_kernel(ReduceArgs a) {
+  constexpr int kRowBatch = 8;
+  __shared__ long long first_row[kThreads];
+  __shared__ int wave_count[kWavesPerBlock];
+  const int pages = collect_pages(a, first_row, wave_count);
+  const int lane = vtx::lane_id();
+  const int wave = threadIdx.x / vtx::kWave;
+  const int R = a.rows_per_tile;
+  const int C = a.cols;
+  const int nv = C / 8;
+  const int tiles = pages * a.heads;
+
+  for (int t = blockIdx.y * kWavesPerBlock + wave; t < tiles; t += gridDim.y * kWavesPerBlock) {
+    const long long row = first_row[t / a.heads] + (t % a.heads);
+    if (row < 0 || row >= a.x_rows || row >= a.out_rows) continue;
+    const uint16_t* tile = a.x + row * (long long)R * C;
+    for (int cv = lane; cv < nv; cv += vtx::kWave) {
+      Acc acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc_init<NEED>(acc[e]);
+      for (int r0 = 0; r0 < R; r0 += kRowBatch) {
+        vtx::U4 v[kRowBatch];
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u)
+          v[u] = r0 + u < R ? vtx::ld16(tile + (long long)(r0 + u) * C + cv * 8) : vtx::U4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          if (r0 + u >= R) break;
+          float f[8];
+          vtx::unpack8(v[u], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc_add<NEED>(acc[e], f[e]);
+        }
+      }
+      const long long elem = row * C + cv * 8;
+#pragma unroll
+      for (int o = 0; o < kMaxOut; ++o) {
+        if (o >= a.n_out) break;
+        uint32_t b[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e] = acc_value(acc[e], a.out_type[o], R);
+        if (a.out_dtype[o] == VTX_DTYPE_BF16) {
+          vtx::st16(reinterpret_cast<uint16_t*>(a.out[o]) + elem,
+                    vtx::U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
+                            b[6] | (b[7] << 16)});
+        } else {
+          uint32_t* dst = reinterpret_cast<uint32_t*>(a.out[o]) + elem;
+          vtx::st16(dst, vtx::U4{b[0] << 16, b[1] << 16, b[2] << 16, b[3] << 16});
+          vtx::st16(dst + 4, vtx::U4{b[4] << 16, b[5] << 16, b[6] << 16, b[7] << 16});
+        }
+      }
+    }
+  }
+}
+
 // Any shape.  dim 1: lanes stride over columns, each lane walks all R rows.
 // dim 2: the wave walks the R rows, lanes stride over columns, a wave
 // reduction finishes each row.
@@ -206,6 +267,7 @@ __global__ __launch_bounds__(kThreads) void reduce_generic_kernel(ReduceArgs a, 
       for (int c = lane; c < C; c += vtx::kWave) {
         Acc acc;
         acc_init(acc);
+#pragma unroll 8
         for (int r = 0; r < R; ++r) acc_add(acc, vtx::bf16_to_f32(tile[(long long)r * C + c]));
 #pragma unroll
         for (int o = 0; o < kMaxOut; ++o)
@@ -291,6 +353,13 @@ int launch_reduce(ReduceArgs& a, int dim, void* stream) {
     launch_vec<32>(a, need, grid, s);
   } else if (vec && lpr == 64) {
     launch_vec<64>(a, need, grid, s);
+  } else if (vec) {
+    switch (need) {
+      case kNeedSum: reduce_colvec_kernel<kNeedSum><<<grid, kThreads, 0, s>>>(a); break;
+      case kNeedMax: reduce_colvec_kernel<kNeedMax><<<grid, kThreads, 0, s>>>(a); break;
+      case kNeedSum | kNeedMax: reduce_colvec_kernel<kNeedSum | kNeedMax><<<grid, kThreads, 0, s>>>(a); break;
+      default: reduce_colvec_kernel<kNeedAll><<<grid, kThreads, 0, s>>>(a); break;
+    }
   } else {
     reduce_generic_kernel<<<grid, kThreads, 0, s>>>(a, dim);
   }

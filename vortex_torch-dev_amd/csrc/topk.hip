@@ -53,22 +53,31 @@ __global__ __launch_bounds__(T) void topk_select_kernel(TopkArgs a) {
   const uint16_t* sc = a.score + start;
 
   if (n <= a.key_cap) {
-    for (long long i = tid; i < n; i += T) keys[i] = (uint16_t)vtx::score_key(sc[i]);
+    constexpr int kU = 4;  // score loads in flight per thread
+    for (long long i0 = 0; i0 < n; i0 += (long long)T * kU) {
+      uint16_t v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const long long i = i0 + (long long)u * T + tid;
+        v[u] = i < n ? sc[i] : (uint16_t)0;
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const long long i = i0 + (long long)u * T + tid;
+        if (i < n) keys[i] = (uint16_t)vtx::score_key(v[u]);
+      }
+    }
     __syncthreads();
     vtx::select_topk<T>([&](long long i) { return (uint32_t)keys[i]; }, n, k, sel, sh);
   } else {
     vtx::select_topk<T>([&](long long i) { return vtx::score_key(sc[i]); }, n, k, sel, sh);
   }
 
-  for (int j = tid; j < k; j += T) {
-    const uint64_t c = sel[j];
-    const long long pos = vtx::sel_position(c);
-    if (pos < n) a.sidx[obase + vtx::rank_of(c, sel, k)] = a.didx[start + pos];
-  }
+  vtx::select_emit<T>(sel, k, n, [&](int r, long long pos) { a.sidx[obase + r] = a.didx[start + pos]; });
 }
 
 constexpr int kMaxTopk = 4096;
-constexpr int kLdsBudget = 60 * 1024;  // dynamic LDS per workgroup
+constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS per workgroup (the select tables take ~6 KB more)
 
 }  // namespace
 

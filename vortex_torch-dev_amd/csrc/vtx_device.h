@@ -62,15 +62,25 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
-// Inclusive suffix sum over lanes: lane l gets sum of v over lanes >= l.
-__device__ __forceinline__ uint32_t wave_suffix_sum(uint32_t v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    uint32_t o = __shfl_down(v, d, kWave);
-    if (l + d < kWave) v += o;
-  }
-  return v;
+// Inclusive prefix sum over the 64 lanes (lane l gets the sum over lanes
+// <= l) with DPP: shifts by 1, 2, 4, 8 inside each 16-lane row, then the
+// last lane of row 0 / row 2 is added to rows 1 / 3 and the last lane of
+// row 1 to rows 2 and 3.  Lanes whose DPP source is outside the row or
+// masked off add 0.  No LDS traffic, unlike lane shuffles.
+__device__ __forceinline__ uint32_t wave_prefix_sum(uint32_t v) {
+  int x = (int)v;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+  return (uint32_t)x;
+}
+
+// Value of v in lane `src` (src wave-uniform), read through a scalar register.
+__device__ __forceinline__ uint32_t lane_value(uint32_t v, int src) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, src);
 }
 
 // 16-byte vector load/store of raw words.

@@ -8,7 +8,14 @@
 //      best item, the number of items above it and how many of the items
 //      equal to it are needed (`take`);
 //   2. items above `thr` win; items equal to `thr` win in position order
-//      (ballot + per-wave counts, tile by tile) until `take` are in.
+//      until `take` are in: per-(tile, wave) tie counts are written once,
+//      after one barrier every wave knows how many ties precede each of its
+//      items.
+//
+// The passes give each thread kSelU items per round with their key reads
+// issued together, and winners are appended with one LDS atomic per wave
+// and round (ballot + prefix), so the cost is a few LDS round trips per
+// pass rather than one per item.
 //
 // Every thread of the workgroup must call it (it contains barriers).
 #pragma once
@@ -17,12 +24,29 @@
 
 namespace vtx {
 
+constexpr int kSelU = 4;          // items per thread per round
+constexpr int kSelTieTiles = 64;  // tiles (of T items) with precomputed tie counts
+
 template <int T>
 struct SelectShared {
   alignas(16) uint32_t hist[2][256];  // read 16 bytes per lane in sel_find_bin_wave
   uint32_t wave_ties[T / kWave];
+  uint32_t tie_counts[kSelTieTiles * (T / kWave)];  // [tile][wave]
   int count;
 };
+
+// Appends this wave's winners (win set) to sel with one LDS atomic for the
+// wave; `comp` is the lane's composite.  Wave-uniform control flow.
+__device__ __forceinline__ void sel_append(bool win, uint64_t comp, uint64_t* sel, int k, int* count) {
+  const uint64_t m = __ballot(win);
+  if (m) {
+    int base = 0;
+    if (lane_id() == 0) base = atomicAdd(count, (int)__popcll(m));
+    base = __builtin_amdgcn_readfirstlane(base);  // lane 0 is active here
+    const int slot = base + lanes_below(m);
+    if (win && slot < k) sel[slot] = comp;
+  }
+}
 
 __device__ __forceinline__ uint64_t sel_composite(uint32_t key, long long pos) {
   return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)pos);
@@ -38,7 +62,8 @@ __device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t
   const int l = lane_id();
   const U4 c = ld16(hist + 4 * l);
   const uint32_t tot = c.x + c.y + c.z + c.w;
-  const uint32_t a3 = wave_suffix_sum(tot) - tot;
+  const uint32_t incl = wave_prefix_sum(tot);
+  const uint32_t a3 = lane_value(incl, kWave - 1) - incl;  // items in the bins of higher lanes
   const uint32_t a2 = a3 + c.w;
   const uint32_t a1 = a2 + c.z;
   const uint32_t a0 = a1 + c.y;
@@ -59,8 +84,8 @@ __device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t
   }
   const uint64_t m = __ballot(b >= 0);
   const int src = m ? (int)__builtin_ctzll(m) : 0;
-  *bin = m ? __shfl(b, src, kWave) : 0;
-  *above = m ? (int)__shfl(ab, src, kWave) : 0;
+  *bin = m ? (int)lane_value((uint32_t)b, src) : 0;
+  *above = m ? (int)lane_value(ab, src) : 0;
 }
 
 // Clears the histograms, the winner count and the winner slots (no barrier).
@@ -97,9 +122,29 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
   sel_find_bin_wave(sh.hist[0], (uint32_t)k, &hi_bin, &above_hi);
   const uint32_t hi = (uint32_t)hi_bin;
 
-  for (long long i = tid; i < n; i += T) {
-    const uint32_t key = key_at(i);
-    if ((key >> 8) == hi) atomicAdd(&sh.hist[1][key & 255u], 1u);
+  // kSelU keys per thread per round, their reads issued together; the keys
+  // of the first round stay in registers for the second pass.
+  auto load = [&](long long i0, uint32_t (&key)[kSelU]) {
+#pragma unroll
+    for (int u = 0; u < kSelU; ++u) {
+      const long long i = i0 + (long long)u * T + tid;
+      key[u] = i < n ? key_at(i) : 0u;
+    }
+  };
+  auto count_lo = [&](long long i0, const uint32_t (&key)[kSelU]) {
+#pragma unroll
+    for (int u = 0; u < kSelU; ++u) {
+      const long long i = i0 + (long long)u * T + tid;
+      if (i < n && (key[u] >> 8) == hi) atomicAdd(&sh.hist[1][key[u] & 255u], 1u);
+    }
+  };
+  uint32_t key0[kSelU];
+  load(0, key0);
+  count_lo(0, key0);
+  for (long long i0 = (long long)T * kSelU; i0 < n; i0 += (long long)T * kSelU) {
+    uint32_t key[kSelU];
+    load(i0, key);
+    count_lo(i0, key);
   }
   __syncthreads();
   int lo_bin = 0, above_lo = 0;
@@ -107,15 +152,57 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
   const uint32_t thr = (hi << 8) | (uint32_t)lo_bin;
   const int take = k - (above_hi + above_lo);  // >= 1 items equal to thr win
   const bool all_ties = (take == (int)sh.hist[1][thr & 255u]);
+  const long long tiles = (n + T - 1) / T;
+  const bool tie_table = !all_ties && tiles <= kSelTieTiles;
 
-  for (long long i = tid; i < n; i += T) {
-    const uint32_t key = key_at(i);
-    if (key > thr || (all_ties && key == thr)) {
-      const int slot = atomicAdd(&sh.count, 1);
-      if (slot < k) sel[slot] = sel_composite(key, i);
+  // Items above the threshold (and, when every tie wins, the ties); the
+  // per-(tile, wave) tie counts are recorded on the way.
+  auto collect = [&](long long i0, const uint32_t (&key)[kSelU]) {
+#pragma unroll
+    for (int u = 0; u < kSelU; ++u) {
+      if (i0 + (long long)u * T >= n) break;  // uniform: the rest of the round is past the end
+      const long long i = i0 + (long long)u * T + tid;
+      const bool in = i < n;
+      const bool win = in && (key[u] > thr || (all_ties && key[u] == thr));
+      sel_append(win, sel_composite(key[u], i), sel, k, &sh.count);
+      if (tie_table) {
+        const uint64_t m = __ballot(in && key[u] == thr);
+        const long long tile = i0 / T + u;
+        if (lane == 0 && tile < tiles) sh.tie_counts[tile * kWaves + wave] = (uint32_t)__popcll(m);
+      }
     }
+  };
+  collect(0, key0);
+  for (long long i0 = (long long)T * kSelU; i0 < n; i0 += (long long)T * kSelU) {
+    uint32_t key[kSelU];
+    load(i0, key);
+    collect(i0, key);
   }
-  if (!all_ties) {
+  if (tie_table) {
+    __syncthreads();
+    // Ties before tile j: sum of earlier tiles' counts; within tile j, the
+    // counts of lower waves, then lower lanes.
+    int before = 0;
+    for (long long j = 0; j < tiles && before < take; ++j) {
+      int tile_total = 0, lower = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const int c = (int)sh.tie_counts[j * kWaves + w];
+        tile_total += c;
+        lower += (w < wave) ? c : 0;
+      }
+      if (tile_total != 0) {
+        const long long i = j * T + tid;
+        const bool eq = i < n && key_at(i) == thr;
+        const uint64_t m = __ballot(eq);
+        const bool tw = eq && before + lower + lanes_below(m) < take;
+        sel_append(tw, sel_composite(thr, i), sel, k, &sh.count);
+      }
+      before += tile_total;
+    }
+  } else if (!all_ties) {
+    // Long segments: tile by tile, with the counts of each tile exchanged
+    // through LDS.
     int seen = 0;  // tied items in earlier tiles
     for (long long t0 = 0; t0 < n; t0 += T) {
       const long long i = t0 + tid;
@@ -130,10 +217,8 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
         before += (w < wave) ? c : 0;
         tile += c;
       }
-      if (eq && before + lanes_below(m) < take) {
-        const int slot = atomicAdd(&sh.count, 1);
-        if (slot < k) sel[slot] = sel_composite(thr, i);
-      }
+      const bool tw = eq && before + lanes_below(m) < take;
+      sel_append(tw, sel_composite(thr, i), sel, k, &sh.count);
       seen += tile;
       __syncthreads();
       if (seen >= take) break;
@@ -153,16 +238,28 @@ __device__ __forceinline__ void select_topk(KeyAt key_at, long long n, int k, ui
   select_topk_counted<T>(key_at, n, k, sel, sh);
 }
 
-// Output rank of winner `c` among the k winners in sel (best = 0).
+// Output rank of winner `c` among the k winners in sel (best = 0): eight
+// 8-byte LDS reads in flight (every lane reads the same composite, a
+// broadcast; 16-byte broadcast reads measured slower on gfx950).
 __device__ __forceinline__ int rank_of(uint64_t c, const uint64_t* sel, int k) {
   int r = 0;
   int m = 0;
-  for (; m + 8 <= k; m += 8) {  // eight independent LDS reads in flight
+  for (; m + 8 <= k; m += 8) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) r += (sel[m + u] > c) ? 1 : 0;
   }
   for (; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
   return r;
+}
+
+// Calls emit(rank, position) for every winner (rank 0 = best).
+template <int T, typename Emit>
+__device__ __forceinline__ void select_emit(const uint64_t* sel, int k, long long n, Emit emit) {
+  for (int j = threadIdx.x; j < k; j += T) {
+    const uint64_t c = sel[j];
+    const long long pos = sel_position(c);
+    if (pos < n) emit(rank_of(c, sel, k), pos);
+  }
 }
 
 }  // namespace vtx

@@ -57,6 +57,18 @@ def fusion_enabled() -> bool:
     return os.environ.get("VORTEX_FUSE", "1") != "0"
 
 
+_LAYOUTS = {"auto": 0, "segment": 1, "split": 2}
+
+
+def fused_layout() -> int:
+    """Work layout of the fused indexer kernel (VORTEX_FUSED_LAYOUT = auto,
+    segment or split; the outputs are the same in every layout)."""
+    name = os.environ.get("VORTEX_FUSED_LAYOUT", "auto")
+    if name not in _LAYOUTS:
+        raise RuntimeError(f"VORTEX_FUSED_LAYOUT must be one of {sorted(_LAYOUTS)}, got {name!r}")
+    return _LAYOUTS[name]
+
+
 class Pending:
     """A recorded computation that writes a tensor's storage when flushed."""
 

@@ -52,7 +52,7 @@ _SIGNATURES = {
     ),
     "vtx_indexer_fused": (
         [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
         ctypes.c_int,
     ),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
@@ -62,6 +62,7 @@ EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
 REDUCE_MEAN, REDUCE_MAX, REDUCE_MIN, REDUCE_L2NORM = 0, 1, 2, 3
 DTYPE_BF16, DTYPE_F32 = 0, 1
+FUSED_AUTO, FUSED_SEGMENT, FUSED_SPLIT = 0, 1, 2
 
 
 def library_path() -> Path:
@@ -390,19 +391,28 @@ def indexer_fused(
     reserved_bos: int,
     reserved_eos: int,
     max_num_pages: int,
+    seg_counters=None,
+    mode: int = FUSED_AUTO,
 ) -> None:
     """q-mean + GeMV + topK of one layer in one launch.
 
     q: bf16 [S, G, D] (the head-group mean is taken in the kernel and written
     to x_out if given) or [S, 1, D] / [S, D] already-averaged rows (G taken as
     0: rows used as they are).  y: centroid pool [rows, 1, D]; score: the GeMV
-    output buffer; the block tables come from the planner.
+    output buffer; the block tables come from the planner.  seg_counters: an
+    int32 buffer of at least S zeros that lets long segments be split over
+    several workgroups (the kernel leaves it zeroed); mode: FUSED_AUTO,
+    FUSED_SEGMENT or FUSED_SPLIT.
     """
     lib = load_library()
     tensors = [q, y, score, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
     if x_out is not None:
         tensors.append(x_out)
+    if seg_counters is not None:
+        tensors.append(seg_counters)
     dev = _require_gpu(*tensors)
+    if seg_counters is not None:
+        _req(seg_counters, torch.int32, "seg_counters")
     _req(q, torch.bfloat16, "q")
     _req(y, torch.bfloat16, "y (centroids)")
     _req(score, torch.bfloat16, "score")
@@ -434,5 +444,7 @@ def indexer_fused(
             dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
             sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), D,
+            seg_counters.data_ptr() if seg_counters is not None else None,
+            seg_counters.numel() if seg_counters is not None else 0, int(mode),
             _stream(dev))
     _check(rc, "indexer_fused")

@@ -36,8 +36,11 @@ class PendingGemv(_deferred.Pending):
         _deferred.materialize(self.x)
         self.op.impl(self.x, self.y, self.op.output_buffer, self.ctx)
 
-    def fuse_with_topk(self, o: torch.Tensor, ctx: Context) -> None:
-        """q-mean (if recorded) + GeMV + topK into ``o`` in one kernel."""
+    def fuse_with_topk(self, o: torch.Tensor, ctx: Context,
+                       seg_counters: Optional[torch.Tensor] = None) -> None:
+        """q-mean (if recorded) + GeMV + topK into ``o`` in one kernel.
+        ``seg_counters`` (the topK op's zeroed int32 buffer, one entry per
+        segment) lets the kernel split long segments over several workgroups."""
         sc = _deferred.current_scope()
         mean = _deferred.pending_of(self.x)
         # earlier recorded work runs first, in program order
@@ -58,7 +61,8 @@ class PendingGemv(_deferred.Pending):
             q, x_out, self.y, self.op.output_buffer,
             ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
             ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
-            ctx.page_reserved_eos, ctx.max_num_pages_per_request)
+            ctx.page_reserved_eos, ctx.max_num_pages_per_request, seg_counters=seg_counters,
+            mode=_deferred.fused_layout())
         if mean is not None:
             mean.done = True
         self.done = True

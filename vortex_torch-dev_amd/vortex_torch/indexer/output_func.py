@@ -33,6 +33,9 @@ class topK(vOp):
     def __init__(self):
         super().__init__()
         self.impl: Optional[Callable] = None
+        # arrival counters of the fused kernel's split layout, one per segment
+        # the block table can hold; zero between launches
+        self.seg_counters: Optional[torch.Tensor] = None
 
     def profile(self, x: vTensor, o: vTensor, ctx: Context) -> None:
         p = self._prefix()
@@ -48,12 +51,15 @@ class topK(vOp):
         self.impl = self._impl_map[x._format]
         assert x.device == o.device, (
             f"{p}x and o must be on the same device (x.device={x.device}, o.device={o.device})")
+        indptr = ctx.dense_kv_indptr
+        if isinstance(indptr, torch.Tensor) and indptr.numel() > 1 and x.device.type == "cuda":
+            self.seg_counters = torch.zeros((indptr.numel() - 1,), dtype=torch.int32, device=x.device)
 
     def execute(self, x: torch.Tensor, o: torch.Tensor, ctx: Context) -> torch.Tensor:
         assert self.impl is not None, f"{self._prefix()}execute called before profile() (impl is None)"
         pending = _deferred.pending_of(x)
         if self.impl is topk_output and isinstance(pending, PendingGemv) and pending.ctx is ctx:
-            pending.fuse_with_topk(o, ctx)
+            pending.fuse_with_topk(o, ctx, self.seg_counters)
             return o
         _deferred.materialize(x)
         self.impl(
