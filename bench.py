@@ -52,8 +52,9 @@ HBM_PEAK_GBPS = 8000.0
 
 # HBM bytes per fused-indexer launch from the FETCH_SIZE and WRITE_SIZE
 # counter passes over --traffic-probe (each scaled by what the counter reads
-# for the probe's copy kernel of known size), keyed by (config, layers).
-TRAFFIC_BYTES_PER_LAUNCH: dict = {}
+# for the probe's copy kernel of known size); the per-launch traffic does not
+# depend on the layer count (34,072 KiB read + 464 KiB written at C2).
+TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_364_864}
 
 
 def _parse():
@@ -346,7 +347,7 @@ def bench_decode(args, dev) -> dict:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(fused_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get((args.config, args.layers)),
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(args.config),
             "us_per_launch": round(us_fused, 3),
             "bytes_per_launch": nbytes["fused"],
         },
