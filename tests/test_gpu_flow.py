@@ -80,6 +80,41 @@ def test_fused_kernel_matches_separate_kernels(gpu, name, mode):
     np.testing.assert_array_equal(_np(sp), exp)
 
 
+@pytest.mark.parametrize("kind", ["ties", "const"])
+@pytest.mark.parametrize("mode", [_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
+def test_fused_kernel_tie_order(gpu, name, mode, kind):
+    """Heavily tied scores: centroid rows drawn from three distinct rows
+    ("ties") or all equal ("const", so every segment selects its first k
+    middle pages).  The selection must be the oracle's stable order of the
+    kernel's own scores: score descending, lower position first."""
+    dev = gpu
+    batch = getattr(W, name)()
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+    S = batch.batch * H
+    rows = batch.pool_pages * H
+    q = W.randn_bf16((S, G, D), 5, dev)
+    base = W.randn_bf16((3, D), 6, dev, std=0.25)
+    if kind == "const":
+        pick = torch.zeros(rows, dtype=torch.long)
+    else:
+        pick = torch.randint(0, 3, (rows,), generator=torch.Generator().manual_seed(7))
+    y = base[pick.to(dev)].view(rows, 1, D).contiguous()
+    qm = torch.empty((S, 1, D), device=dev, dtype=torch.bfloat16)
+    sc = torch.zeros((ic.dense_kv_indices.numel(), 1, 1), device=dev, dtype=torch.bfloat16)
+    sp = ic.sparse_kv_indices.clone()
+    counters = torch.zeros(S, dtype=torch.int32, device=dev)
+    _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp,
+                       S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request,
+                       seg_counters=counters, mode=mode)
+    torch.cuda.synchronize()
+    exp, _ = O.topk(_bits(sc), _np(ic.dense_kv_indptr), _np(ic.sparse_kv_indptr), _np(ic.dense_kv_indices),
+                    _np(ic.sparse_kv_indices), S, batch.topk, batch.bos, batch.eos)
+    np.testing.assert_array_equal(_np(sp), exp)
+
+
 @pytest.mark.parametrize("mode", [_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT])
 def test_fused_kernel_extra_query_rows(gpu, mode):
     # more query rows than segments (padded batch): every row gets its mean

@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kThreads, (VPL == 1 ? 4 : 2)) void gemv_paged_kerne
           live[ii] = r >= 0;
           const uint16_t* yr = a.y + (long long)(live[ii] ? r : fallback) * a.dim;
 #pragma unroll
-          for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16(yr + (v * LPR + col) * 8);
+          for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16_stream(yr + (v * LPR + col) * 8);
         }
 #pragma unroll
         for (int ii = 0; ii < kBatch; ++ii) {

@@ -149,7 +149,7 @@ __device__ __forceinline__ float score_pass(const FusedArgs& a, int my_row, int 
       if ((i0 + ii) * kRowsPerLoad < cnt) {  // wave-uniform: slots past the pass are skipped
         const uint16_t* yr = a.y + (long long)(live[ii] ? row : first) * D;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16(yr + (v * LPR + col) * 8);
+        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16_stream(yr + (v * LPR + col) * 8);
       } else {
 #pragma unroll
         for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::U4{0u, 0u, 0u, 0u};

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_vec_kernel(ReduceArgs a)
     for (int e = 0; e < 8; ++e) acc_init<NEED>(acc[e]);
 #pragma unroll 4
     for (int r = grp; r < R; r += kGroups) {
-      const vtx::U4 v = vtx::ld16(base + (long long)r * a.cols);
+      const vtx::U4 v = vtx::ld16_stream(base + (long long)r * a.cols);
       acc_add<NEED>(acc[0], vtx::bf16_lo(v.x));
       acc_add<NEED>(acc[1], vtx::bf16_hi(v.x));
       acc_add<NEED>(acc[2], vtx::bf16_lo(v.y));
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kThreads) void reduce_colvec_kernel(ReduceArgs a) {
         vtx::U4 v[kRowBatch];
 #pragma unroll
         for (int u = 0; u < kRowBatch; ++u)
-          v[u] = r0 + u < R ? vtx::ld16(tile + (long long)(r0 + u) * C + cv * 8) : vtx::U4{0u, 0u, 0u, 0u};
+          v[u] = r0 + u < R ? vtx::ld16_stream(tile + (long long)(r0 + u) * C + cv * 8) : vtx::U4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int u = 0; u < kRowBatch; ++u) {
           if (r0 + u >= R) break;
