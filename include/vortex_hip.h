@@ -176,6 +176,7 @@ int vtx_indexer_fused_supported(int32_t head_dim);
 #define VTX_REDUCE_MAX 1
 #define VTX_REDUCE_MIN 2
 #define VTX_REDUCE_L2NORM 3
+#define VTX_REDUCE_SUM 4
 
 /* Output element types. */
 #define VTX_DTYPE_BF16 0
@@ -213,6 +214,118 @@ int vtx_page_reduce_multi(const uint16_t* x, int64_t x_rows,
                           const int32_t* reduce_types, int64_t out_rows,
                           const int64_t* loc, int64_t nnz, int32_t num_kv_heads,
                           int32_t page_size, int32_t dim, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Workload-walking indexer ops (GeMM, elementwise, reductions, segment
+ * softmax / normalize): the ops of the GQA and Quest flows.
+ *
+ * Each visits exactly the packed positions of the planner's workload list:
+ * workload w < min(*winfo_num_workloads, winfo_capacity) covers
+ * winfo_kv_lens[w] positions from winfo_kv_offsets[w], of segment
+ * winfo_q_indices[w].  An operand's row at position p is, by row mode,
+ *   VTX_ROWS_BATCHED: winfo_q_indices[w]   (query rows [S, d0, d1])
+ *   VTX_ROWS_PAGED:   dense_kv_indices[p]  (a cache pool [rows, d0, d1])
+ *   VTX_ROWS_RAGGED:  p                    (a per-position buffer)
+ * and the output row is p.  Operands and outputs are bf16 tiles [d0, d1]
+ * per row; positions outside the workloads are not written; a row outside
+ * its operand's `rows` is skipped.  Compute is fp32, results rounded to bf16.
+ * ---------------------------------------------------------------------- */
+#define VTX_ROWS_BATCHED 0
+#define VTX_ROWS_PAGED 1
+#define VTX_ROWS_RAGGED 2
+
+/* Values of the reference's ElementwiseBinaryOpType (vortex_torch/utils.py:19-23). */
+#define VTX_BINARY_MAXIMUM 0
+#define VTX_BINARY_MINIMUM 1
+#define VTX_BINARY_ADD 2
+#define VTX_BINARY_MUL 3
+
+/* Values of the reference's ElementwiseOpType (vortex_torch/utils.py:26-31). */
+#define VTX_UNARY_RELU 0
+#define VTX_UNARY_SIGMOID 1
+#define VTX_UNARY_SILU 2
+#define VTX_UNARY_ABS 3
+#define VTX_UNARY_ADD_MUL 4
+
+/*
+ * o[p, c, g] = bf16(fp32 sum_k x[rx, g, k] * y[ry, c, k]); o is
+ * [o_rows, y_d0, x_d0], K = k (a multiple of 8).  x: BATCHED or RAGGED;
+ * y: PAGED or RAGGED.
+ * Replaces mm_bpr / mm_rrr / mm_rpr (reference
+ * vortex_torch/indexer/triton_kernels/matmul_impl.py:6-113, 127-391) behind
+ * GeMM (vortex_torch/indexer/matmul.py:193-398).
+ */
+int vtx_ragged_gemm(const uint16_t* x, int64_t x_rows, int32_t x_mode, int32_t x_d0,
+                    const uint16_t* y, int64_t y_rows, int32_t y_mode, int32_t y_d0, int32_t k,
+                    uint16_t* o, int64_t o_rows, const int32_t* dense_kv_indices,
+                    int64_t dense_kv_indices_len, const int32_t* winfo_q_indices,
+                    const int32_t* winfo_kv_offsets, const int32_t* winfo_kv_lens,
+                    int64_t winfo_capacity, const int32_t* winfo_num_workloads, void* stream);
+
+/*
+ * o[p, i, j] = op(x[rx, i, j], y[ry, i, j]) with size-1 operand axes
+ * broadcast to the output tile [o_d0, o_d1].  MAXIMUM / MINIMUM compare the
+ * values, MUL rounds the product, ADD rounds bf16(alpha)*x and bf16(beta)*y
+ * to bf16 and then their sum.  x: BATCHED or RAGGED; y: PAGED or RAGGED.
+ * Replaces elementwise_binary_{bpr,rrr,rpr} (reference
+ * vortex_torch/indexer/triton_kernels/elementwise_binary_impl.py:7-510)
+ * behind Maximum / Minimum / Add / Multiply
+ * (vortex_torch/indexer/elementwise_binary.py:8-326).
+ */
+int vtx_ragged_binary(int32_t op, float alpha, float beta, const uint16_t* x, int64_t x_rows,
+                      int32_t x_mode, int32_t x_d0, int32_t x_d1, const uint16_t* y, int64_t y_rows,
+                      int32_t y_mode, int32_t y_d0, int32_t y_d1, uint16_t* o, int64_t o_rows,
+                      int32_t o_d0, int32_t o_d1, const int32_t* dense_kv_indices,
+                      int64_t dense_kv_indices_len, const int32_t* winfo_q_indices,
+                      const int32_t* winfo_kv_offsets, const int32_t* winfo_kv_lens,
+                      int64_t winfo_capacity, const int32_t* winfo_num_workloads, void* stream);
+
+/*
+ * o[p] = op(x[p]) elementwise on RAGGED rows, tile [d0, d1], with
+ * a = bf16(alpha), b = bf16(beta), z = bf16(bf16(b*x) + a):
+ * RELU x >= a ? x : b; SIGMOID 1/(1+exp(z)); SILU x/(1+exp(z)); ABS |z|;
+ * ADD_MUL z.
+ * Replaces elementwise_rr (reference
+ * vortex_torch/indexer/triton_kernels/elementwise_impl.py:7-171) behind
+ * Relu / Sigmoid / Silu / Abs / Add_Mul (vortex_torch/indexer/elementwise.py).
+ */
+int vtx_ragged_unary(int32_t op, float alpha, float beta, const uint16_t* x, int64_t x_rows,
+                     int32_t d0, int32_t d1, uint16_t* o, int64_t o_rows,
+                     const int32_t* winfo_kv_offsets, const int32_t* winfo_kv_lens,
+                     int64_t winfo_capacity, const int32_t* winfo_num_workloads, void* stream);
+
+/*
+ * o[p] = reduction of the RAGGED tile x[p] ([d0, d1]) over axis dim (1: d0,
+ * o is [o_rows, 1, d1]; 2: d1, o is [o_rows, d0, 1]): MEAN (sum / count),
+ * MAX, MIN, L2NORM (sqrt of the sum of squares) or SUM, in fp32.
+ * Replaces reduce_rr (reference
+ * vortex_torch/indexer/triton_kernels/reduce_impl.py:8-146) behind
+ * Max / Mean / Min / L2Norm / Sum (vortex_torch/indexer/reduce.py:8-438).
+ */
+int vtx_ragged_reduce(const uint16_t* x, int64_t x_rows, int32_t d0, int32_t d1, uint16_t* o,
+                      int64_t o_rows, int32_t dim, int32_t reduce_type,
+                      const int32_t* winfo_kv_offsets, const int32_t* winfo_kv_lens,
+                      int64_t winfo_capacity, const int32_t* winfo_num_workloads, void* stream);
+
+#define VTX_SEGMENT_SOFTMAX 0
+#define VTX_SEGMENT_NORMALIZE 1
+
+/*
+ * In place, for every segment s < eff_batch_size whose page count
+ * n = dense_kv_indptr[s+1] - dense_kv_indptr[s] exceeds
+ * reserved_bos + reserved_eos + topk_val, over its middle positions
+ * [indptr[s] + bos, indptr[s+1] - eos) and each of the `cols` values of a
+ * position's tile, independently per column:
+ *   SOFTMAX:   x = bf16(exp(v - max v) / sum exp(v - max v)), v = x * scale
+ *   NORMALIZE: x = bf16(x / max(sqrt(sum x^2), 1e-12))
+ * Replaces softmax_inplace_r / normalize_inplace_r (reference
+ * vortex_torch/indexer/triton_kernels/softmax_impl.py:6-130,
+ * normalize_impl.py:6-118) behind Softmax / Normalize
+ * (vortex_torch/indexer/scan.py:8-388).
+ */
+int vtx_segment_scan(int32_t op, float scale, uint16_t* x, int64_t x_rows, int32_t cols,
+                     const int32_t* dense_kv_indptr, int32_t eff_batch_size, int32_t topk_val,
+                     int32_t reserved_bos, int32_t reserved_eos, void* stream);
 
 #ifdef __cplusplus
 }

@@ -278,3 +278,185 @@ def q_group_mean(q_bits) -> np.ndarray:
     """[S, G, D] bf16 bits -> [S, 1, D] bf16 bits (fp32-accurate mean)."""
     q = bf16_to_f32(q_bits).astype(np.float64)
     return f32_to_bf16(q.mean(axis=1, keepdims=True).astype(np.float32))
+
+
+# --------------------------------------------------------------------------
+# A.5 workload-walking indexer ops of the GQA and Quest flows
+#     GeMM       indexer/triton_kernels/matmul_impl.py:6-113 (bpr), 127-391 (rrr, rpr)
+#     binary     indexer/triton_kernels/elementwise_binary_impl.py:7-510
+#     unary      indexer/triton_kernels/elementwise_impl.py:7-171
+#     reduce     indexer/triton_kernels/reduce_impl.py:8-146
+#     softmax    indexer/triton_kernels/softmax_impl.py:6-130
+#     normalize  indexer/triton_kernels/normalize_impl.py:6-118
+# Row modes (the reference's FORMAT pairs): 0 BATCHED -> the workload's
+# segment, 1 PAGED -> dense_indices[p], 2 RAGGED -> p.
+# --------------------------------------------------------------------------
+
+ROWS_BATCHED, ROWS_PAGED, ROWS_RAGGED = 0, 1, 2
+
+
+def workload_positions(winfo_q, winfo_off, winfo_len, num_workloads: int):
+    """(p, q) of every position the workload list covers, in workload order."""
+    nw = int(num_workloads)
+    lens = np.asarray(winfo_len[:nw], dtype=np.int64)
+    offs = np.asarray(winfo_off[:nw], dtype=np.int64)
+    qs = np.asarray(winfo_q[:nw], dtype=np.int64) if winfo_q is not None else np.zeros(nw, np.int64)
+    first = np.repeat(np.cumsum(lens) - lens, lens)
+    p = np.repeat(offs, lens) + (np.arange(int(lens.sum())) - first)
+    return p, np.repeat(qs, lens)
+
+
+def _rows_of(mode: int, p, q, dense_indices):
+    if mode == ROWS_BATCHED:
+        return q
+    if mode == ROWS_PAGED:
+        return np.asarray(dense_indices, dtype=np.int64)[p]
+    return p
+
+
+def _tile3(bits):
+    a = np.asarray(bits)
+    return a if a.ndim == 3 else a.reshape(a.shape[0], 1, -1)
+
+
+def ragged_gemm(x_bits, x_mode: int, y_bits, y_mode: int, out_bits, dense_indices, winfo_q, winfo_off,
+                winfo_len, num_workloads: int):
+    """o[p, c, g] = sum_k x[rx, g, k] * y[ry, c, k] (float64, rounded once to
+    fp32 then bf16) at every covered position; returns (out bits, covered)."""
+    x = bf16_to_f32(_tile3(x_bits)).astype(np.float64)
+    y = bf16_to_f32(_tile3(y_bits)).astype(np.float64)
+    out = np.array(_tile3(out_bits), copy=True)
+    covered = np.zeros(out.shape[0], dtype=bool)
+    p, q = workload_positions(winfo_q, winfo_off, winfo_len, num_workloads)
+    if p.size == 0:
+        return out, covered
+    v = np.einsum("pgk,pck->pcg", x[_rows_of(x_mode, p, q, dense_indices)], y[_rows_of(y_mode, p, q, dense_indices)])
+    out[p] = f32_to_bf16(v.astype(np.float32)).reshape(out[p].shape)
+    covered[p] = True
+    return out, covered
+
+
+def _bf16_round(v):
+    return bf16_to_f32(f32_to_bf16(np.asarray(v, dtype=np.float32))).astype(np.float64)
+
+
+BINARY_MAXIMUM, BINARY_MINIMUM, BINARY_ADD, BINARY_MUL = 0, 1, 2, 3
+
+
+def ragged_binary(op: int, alpha: float, beta: float, x_bits, x_mode: int, y_bits, y_mode: int, out_bits,
+                  dense_indices, winfo_q, winfo_off, winfo_len, num_workloads: int):
+    """o[p] = op(x[rx], y[ry]) with size-1 tile axes broadcast; bf16
+    arithmetic: max/min of the values, mul = bf16(x*y), add = bf16(bf16(a*x)
+    + bf16(b*y)) with a, b = bf16(alpha), bf16(beta).  Returns (out, covered)."""
+    x = bf16_to_f32(_tile3(x_bits)).astype(np.float64)
+    y = bf16_to_f32(_tile3(y_bits)).astype(np.float64)
+    out = np.array(_tile3(out_bits), copy=True)
+    covered = np.zeros(out.shape[0], dtype=bool)
+    p, q = workload_positions(winfo_q, winfo_off, winfo_len, num_workloads)
+    if p.size == 0:
+        return out, covered
+    xs = x[_rows_of(x_mode, p, q, dense_indices)]
+    ys = y[_rows_of(y_mode, p, q, dense_indices)]
+    if op == BINARY_MAXIMUM:
+        v = np.maximum(xs, ys)
+    elif op == BINARY_MINIMUM:
+        v = np.minimum(xs, ys)
+    elif op == BINARY_ADD:
+        a, b = _bf16_round(alpha), _bf16_round(beta)
+        v = _bf16_round(a * xs) + _bf16_round(b * ys)
+    else:
+        v = xs * ys
+    out[p] = f32_to_bf16(np.broadcast_to(v, (p.size,) + out.shape[1:]).astype(np.float32))
+    covered[p] = True
+    return out, covered
+
+
+UNARY_RELU, UNARY_SIGMOID, UNARY_SILU, UNARY_ABS, UNARY_ADD_MUL = 0, 1, 2, 3, 4
+
+
+def ragged_unary(op: int, alpha: float, beta: float, x_bits, out_bits, winfo_off, winfo_len, num_workloads: int):
+    """Elementwise op on RAGGED rows with a = bf16(alpha), b = bf16(beta),
+    z = bf16(bf16(b*x) + a): relu x >= a ? x : b; sigmoid 1/(1+exp(z)); silu
+    x/(1+exp(z)); abs |z|; add_mul z.  Returns (out, covered)."""
+    x = bf16_to_f32(_tile3(x_bits)).astype(np.float64)
+    out = np.array(_tile3(out_bits), copy=True)
+    covered = np.zeros(out.shape[0], dtype=bool)
+    p, _ = workload_positions(None, winfo_off, winfo_len, num_workloads)
+    if p.size == 0:
+        return out, covered
+    xs = x[p]
+    a, b = _bf16_round(alpha), _bf16_round(beta)
+    z = _bf16_round(_bf16_round(b * xs) + a)
+    with np.errstate(over="ignore"):
+        if op == UNARY_RELU:
+            v = np.where(xs >= a, xs, b)
+        elif op == UNARY_SIGMOID:
+            v = 1.0 / (1.0 + np.exp(z))
+        elif op == UNARY_SILU:
+            v = xs / (1.0 + np.exp(z))
+        elif op == UNARY_ABS:
+            v = np.abs(z)
+        else:
+            v = z
+    out[p] = f32_to_bf16(v.astype(np.float32))
+    covered[p] = True
+    return out, covered
+
+
+REDUCE_SUM = 4
+
+
+def ragged_reduce(x_bits, out_bits, dim: int, reduce_type: int, winfo_off, winfo_len, num_workloads: int):
+    """o[p] = reduction of the tile x[p] over axis dim (1 -> [1, D1], 2 ->
+    [D0, 1]): mean, max, min, L2 = sqrt(sum x^2), sum (float64, rounded once).
+    Returns (out, covered)."""
+    x = bf16_to_f32(_tile3(x_bits)).astype(np.float64)
+    out = np.array(out_bits, copy=True)
+    covered = np.zeros(out.shape[0], dtype=bool)
+    p, _ = workload_positions(None, winfo_off, winfo_len, num_workloads)
+    if p.size == 0:
+        return out, covered
+    t = x[p]
+    ax = 1 if dim == 1 else 2
+    if reduce_type == MEAN:
+        v = t.mean(axis=ax, keepdims=True)
+    elif reduce_type == MAX:
+        v = t.max(axis=ax, keepdims=True)
+    elif reduce_type == MIN:
+        v = t.min(axis=ax, keepdims=True)
+    elif reduce_type == L2NORM:
+        v = np.sqrt((t * t).sum(axis=ax, keepdims=True))
+    else:
+        v = t.sum(axis=ax, keepdims=True)
+    out[p] = f32_to_bf16(v.astype(np.float32)).reshape(out[p].shape)
+    covered[p] = True
+    return out, covered
+
+
+SEGMENT_SOFTMAX, SEGMENT_NORMALIZE = 0, 1
+
+
+def segment_scan(op: int, scale: float, x_bits, dense_indptr, eff_batch_size: int, topk_val: int, bos: int,
+                 eos: int):
+    """In place (on a copy) per segment with n > bos + eos + topk_val pages,
+    over the middle positions and per tile column: softmax of
+    fp32(x) * fp32(scale), or x / max(||x||_2, 1e-12).  Returns (out, touched)."""
+    out = np.array(x_bits, copy=True)
+    flat = out.reshape(out.shape[0], -1)
+    touched = np.zeros(out.shape[0], dtype=bool)
+    dip = np.asarray(dense_indptr, dtype=np.int64)
+    for s in range(int(eff_batch_size)):
+        n = dip[s + 1] - dip[s]
+        if n <= bos + eos + topk_val:
+            continue
+        a, b = dip[s] + bos, dip[s + 1] - eos
+        v = bf16_to_f32(flat[a:b]).astype(np.float64)
+        if op == SEGMENT_SOFTMAX:
+            u = (bf16_to_f32(flat[a:b]) * np.float32(scale)).astype(np.float64)
+            e = np.exp(u - u.max(axis=0, keepdims=True))
+            r = e / e.sum(axis=0, keepdims=True)
+        else:
+            r = v / np.maximum(np.sqrt((v * v).sum(axis=0, keepdims=True)), 1e-12)
+        flat[a:b] = f32_to_bf16(r.astype(np.float32))
+        touched[a:b] = True
+    return out, touched

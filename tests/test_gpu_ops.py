@@ -1,0 +1,293 @@
+"""GPU parity of the workload-walking indexer ops (GeMM, elementwise,
+tile reductions, segment softmax / normalize) and of the GQA and Quest flows
+run through the public API.
+
+Each kernel is called through the C ABI on the planner's own block tables
+(C1, C2, C5 and random small layouts) and compared with the oracle on the
+same inputs: bit-exact for max / min / mul / add, relu / abs / add_mul and
+the max / min reductions; within rtol 1e-2 / atol 1e-3 for the fp32
+contractions and sums (GeMM, mean, sum, L2) and the exp-based ops (softmax,
+sigmoid, SiLU; atol 1e-6 for softmax probabilities).  Positions outside the
+workload list must keep their sentinel.  The flows' selections are
+bit-exact against the oracle top-k of the GPU's own page scores.
+"""
+import numpy as np
+import pytest
+import torch
+
+import workloads as W
+from oracle import vortex_oracle as O
+from vortex_torch import _hip
+from vortex_torch.abs import FORMAT, as_vtensor
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = -7.0
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _bits(t):
+    with torch._C.DisableTorchFunctionSubclass():
+        return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _f(bits):
+    return O.bf16_to_f32(bits)
+
+
+def _planned(name, dev):
+    from vortex_torch.indexer.utils_sglang import plan_decode
+
+    batch = W.random_small(int(name[1:])) if name.startswith("r") else getattr(W, name)()
+    ic, cc = W.make_contexts(batch, dev)
+    b = batch.to(dev)
+    plan_decode(b.seq_lens, b.req_to_token, b.req_indices, ic)
+    return batch, ic, cc
+
+
+def _winfo(ic):
+    return (ic.winfo_q_indices, ic.winfo_kv_offsets, ic.winfo_kv_lens, ic.winfo_num_workloads)
+
+
+def _owinfo(ic):
+    return (_np(ic.winfo_q_indices), _np(ic.winfo_kv_offsets), _np(ic.winfo_kv_lens),
+            int(ic.winfo_num_workloads.item()))
+
+
+def _sentinel(shape, dev):
+    return torch.full(shape, SENTINEL, device=dev, dtype=torch.bfloat16)
+
+
+def _close(got_bits, exp_bits, covered, rtol=1e-2, atol=1e-3):
+    got, exp = _f(got_bits), _f(exp_bits)
+    np.testing.assert_allclose(got[covered], exp[covered], rtol=rtol, atol=atol)
+    assert (got[~covered] == SENTINEL).all(), "a position outside the workload list was written"
+
+
+LAYOUTS = ["c1", "c2", "c5", "r3", "r11"]
+
+
+@pytest.mark.parametrize("name", LAYOUTS)
+def test_gemm_bpr_matches_oracle(gpu, name):
+    batch, ic, _ = _planned(name, gpu)
+    H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+    q = W.randn_bf16((batch.batch * H, G, D), 1, gpu)
+    cen = W.randn_bf16((batch.pool_pages * H, 1, D), 2, gpu, std=0.25)
+    o = _sentinel((ic.dense_kv_indices.numel(), 1, G), gpu)
+    _hip.ragged_gemm(q, _hip.ROWS_BATCHED, cen, _hip.ROWS_PAGED, o, ic.dense_kv_indices, _winfo(ic))
+    exp, cov = O.ragged_gemm(_bits(q), O.ROWS_BATCHED, _bits(cen), O.ROWS_PAGED, _bits(o), _np(ic.dense_kv_indices),
+                             *_owinfo(ic))
+    assert cov.any() or int(ic.winfo_num_workloads.item()) == 0
+    _close(_bits(o), exp, cov)
+
+
+@pytest.mark.parametrize("modes", [(_hip.ROWS_RAGGED, _hip.ROWS_RAGGED), (_hip.ROWS_RAGGED, _hip.ROWS_PAGED),
+                                   (_hip.ROWS_BATCHED, _hip.ROWS_PAGED)])
+@pytest.mark.parametrize("K", [64, 72, 128, 576])
+def test_gemm_modes_and_tiles(gpu, modes, K):
+    batch, ic, _ = _planned("r5", gpu)
+    S, H = ic.dense_kv_indices.numel(), batch.num_kv_heads
+    xm, ym = modes
+    C, G = 2, 3
+    x = W.randn_bf16((batch.batch * H if xm == _hip.ROWS_BATCHED else S, G, K), 3, gpu)
+    y = W.randn_bf16((batch.pool_pages * H if ym == _hip.ROWS_PAGED else S, C, K), 4, gpu, std=0.5)
+    o = _sentinel((S, C, G), gpu)
+    _hip.ragged_gemm(x, xm, y, ym, o, ic.dense_kv_indices, _winfo(ic))
+    exp, cov = O.ragged_gemm(_bits(x), xm, _bits(y), ym, _bits(o), _np(ic.dense_kv_indices), *_owinfo(ic))
+    _close(_bits(o), exp, cov)
+
+
+@pytest.mark.parametrize("op", [O.BINARY_MAXIMUM, O.BINARY_MINIMUM, O.BINARY_ADD, O.BINARY_MUL])
+@pytest.mark.parametrize("case", ["bpr_quest", "rrr", "rpr_bcast", "rrr_scalar_cols"])
+def test_binary_matches_oracle_bit_exact(gpu, op, case):
+    batch, ic, _ = _planned("c1" if case == "bpr_quest" else "r7", gpu)
+    S, H, G = ic.dense_kv_indices.numel(), batch.num_kv_heads, batch.group_size
+    D = 128
+    if case == "bpr_quest":  # Multiply(q, cache["max"]) of the Quest flow
+        xm, ym, xs, ys, os_ = _hip.ROWS_BATCHED, _hip.ROWS_PAGED, (batch.batch * H, G, D), (batch.pool_pages * H, 1, D), (S, G, D)
+    elif case == "rrr":
+        xm, ym, xs, ys, os_ = _hip.ROWS_RAGGED, _hip.ROWS_RAGGED, (S, 3, 16), (S, 3, 16), (S, 3, 16)
+    elif case == "rpr_bcast":
+        xm, ym, xs, ys, os_ = _hip.ROWS_RAGGED, _hip.ROWS_PAGED, (S, 3, 1), (batch.pool_pages * H, 1, 16), (S, 3, 16)
+    else:
+        xm, ym, xs, ys, os_ = _hip.ROWS_RAGGED, _hip.ROWS_RAGGED, (S, 2, 3), (S, 1, 3), (S, 2, 3)
+    x, y = W.randn_bf16(xs, 5, gpu), W.randn_bf16(ys, 6, gpu)
+    o = _sentinel(os_, gpu)
+    alpha, beta = 0.7, -1.3
+    _hip.ragged_binary(op, alpha, beta, x, xm, y, ym, o, ic.dense_kv_indices, _winfo(ic))
+    exp, cov = O.ragged_binary(op, alpha, beta, _bits(x), xm, _bits(y), ym, _bits(o), _np(ic.dense_kv_indices),
+                               *_owinfo(ic))
+    np.testing.assert_array_equal(_bits(o), exp)
+
+
+@pytest.mark.parametrize("op", [O.UNARY_RELU, O.UNARY_SIGMOID, O.UNARY_SILU, O.UNARY_ABS, O.UNARY_ADD_MUL])
+@pytest.mark.parametrize("tile", [(2, 16), (3, 5)])
+def test_unary_matches_oracle(gpu, op, tile):
+    batch, ic, _ = _planned("r9", gpu)
+    S = ic.dense_kv_indices.numel()
+    x = W.randn_bf16((S,) + tile, 7, gpu, std=3.0)
+    o = _sentinel((S,) + tile, gpu)
+    _hip.ragged_unary(op, 0.3, -0.8, x, o, _winfo(ic))
+    _, woff, wlen, nw = _owinfo(ic)
+    exp, cov = O.ragged_unary(op, 0.3, -0.8, _bits(x), _bits(o), woff, wlen, nw)
+    if op in (O.UNARY_SIGMOID, O.UNARY_SILU):
+        _close(_bits(o), exp, cov)
+    else:
+        np.testing.assert_array_equal(_bits(o), exp)
+
+
+@pytest.mark.parametrize("rtype", [O.MEAN, O.MAX, O.MIN, O.L2NORM, O.REDUCE_SUM])
+@pytest.mark.parametrize("dim", [1, 2])
+@pytest.mark.parametrize("tile", [(1, 2), (2, 128), (3, 5)])
+def test_reduce_matches_oracle(gpu, rtype, dim, tile):
+    batch, ic, _ = _planned("c2" if tile == (1, 2) else "r4", gpu)
+    S = ic.dense_kv_indices.numel()
+    x = W.randn_bf16((S,) + tile, 8, gpu)
+    oshape = (S, 1, tile[1]) if dim == 1 else (S, tile[0], 1)
+    o = _sentinel(oshape, gpu)
+    _hip.ragged_reduce(x, o, dim, rtype, _winfo(ic))
+    _, woff, wlen, nw = _owinfo(ic)
+    exp, cov = O.ragged_reduce(_bits(x), _bits(o), dim, rtype, woff, wlen, nw)
+    if rtype in (O.MAX, O.MIN):
+        np.testing.assert_array_equal(_bits(o), exp)
+    else:
+        _close(_bits(o), exp, cov)
+
+
+@pytest.mark.parametrize("op", [O.SEGMENT_SOFTMAX, O.SEGMENT_NORMALIZE])
+@pytest.mark.parametrize("name,cols", [("c1", 2), ("c2", 2), ("c5", 16), ("r6", 3), ("r6", 300)])
+def test_segment_scan_matches_oracle(gpu, op, name, cols):
+    batch, ic, _ = _planned(name, gpu)
+    S = ic.dense_kv_indices.numel()
+    E = batch.batch * batch.num_kv_heads
+    x = W.randn_bf16((S, 1, cols), 9, gpu, std=4.0)
+    before = _bits(x).copy()
+    _hip.segment_scan(op, 0.09, x, ic.dense_kv_indptr, E, batch.topk, batch.bos, batch.eos)
+    exp, touched = O.segment_scan(op, 0.09, before, _np(ic.dense_kv_indptr), E, batch.topk, batch.bos, batch.eos)
+    got = _bits(x)
+    np.testing.assert_array_equal(got[~touched], before[~touched])
+    np.testing.assert_allclose(_f(got[touched]), _f(exp[touched]), rtol=1e-2,
+                               atol=1e-6 if op == O.SEGMENT_SOFTMAX else 1e-3)
+
+
+# ----------------------------------------------------------------- flows
+class _Flow:
+    """One layer of a registered flow on `batch`, through the public API."""
+
+    def __init__(self, flow_name, batch, dev, seed=0):
+        from vortex_torch import flow as vflow
+
+        self.batch, self.dev = batch, dev
+        self.ic, self.cc = W.make_contexts(batch, dev)
+        H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+        self.flow = vflow.build_vflow(flow_name)
+        rows = batch.pool_pages * H
+        self.k = W.randn_bf16((rows, P, D), seed, dev)
+        self.cache = {"k": as_vtensor(self.k, FORMAT.PAGED)}
+        for name, (r, c) in self.flow.create_cache(P, D).items():
+            self.cache[name] = as_vtensor(W.randn_bf16((rows, r, c), seed + 1 + len(self.cache), dev, std=0.25),
+                                          FORMAT.PAGED)
+        self.q = as_vtensor(W.randn_bf16((batch.batch * H, G, D), seed + 9, dev), FORMAT.BATCHED)
+        self.o = as_vtensor(self.ic.sparse_kv_indices.view(-1, 1, 1), FORMAT.RAGGED)
+        self.loc = W.decode_loc(batch).to(dev)
+        self.dev_batch = batch.to(dev)
+        self.ic.profile()
+        self.cc.profile()
+        self.flow.forward_cache(self.cache, self.loc, self.cc)
+        self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
+        self.ic.execute()
+        self.cc.execute()
+
+    def step(self):
+        from vortex_torch.indexer.utils_sglang import plan_decode
+
+        b = self.dev_batch
+        plan_decode(b.seq_lens, b.req_to_token, b.req_indices, self.ic)
+        self.flow.forward_cache(self.cache, self.loc, self.cc)
+        self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
+
+
+def _check_selection(run, page_score_bits):
+    ic, b = run.ic, run.batch
+    sel, _ = O.topk(page_score_bits.reshape(-1), _np(ic.dense_kv_indptr), _np(ic.sparse_kv_indptr),
+                    _np(ic.dense_kv_indices), _np(ic.sparse_kv_indices), b.batch * b.num_kv_heads, b.topk, b.bos,
+                    b.eos)
+    np.testing.assert_array_equal(_np(ic.sparse_kv_indices), sel)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "r3"])
+def test_gqa_block_sparse_flow(gpu, name):
+    batch = W.random_small(3) if name == "r3" else getattr(W, name)()
+    run = _Flow("gqa_block_sparse_attention", batch, gpu)
+    run.step()
+    torch.cuda.synchronize()
+    f, ic = run.flow, run.ic
+    cov = np.zeros(ic.dense_kv_indices.numel(), bool)
+    p, _ = O.workload_positions(*_owinfo(ic))
+    cov[p] = True
+    # stage by stage on the GPU's own intermediates: GeMM, softmax, max over G
+    raw, _ = O.ragged_gemm(_bits(run.q), O.ROWS_BATCHED, _bits(run.cache["centroids"]), O.ROWS_PAGED,
+                           np.zeros(tuple(f.gemm.output_buffer.shape), np.uint16), _np(ic.dense_kv_indices),
+                           *_owinfo(ic))
+    sm = _bits(f.gemm.output_buffer)  # softmax ran in place on the GeMM output
+    exp_sm, touched = O.segment_scan(O.SEGMENT_SOFTMAX, 0.09, raw, _np(ic.dense_kv_indptr),
+                                     batch.batch * batch.num_kv_heads, batch.topk, batch.bos, batch.eos)
+    np.testing.assert_allclose(_f(sm[touched]), _f(exp_sm[touched]), rtol=2e-2, atol=1e-5)
+    aggr = _bits(f.max_op.output_buffer)
+    exp_aggr, _ = O.ragged_reduce(sm, aggr, 2, O.MAX, *_owinfo(ic)[1:])
+    np.testing.assert_array_equal(aggr[cov], exp_aggr[cov])
+    _check_selection(run, aggr)
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "r3"])
+def test_gqa_quest_flow(gpu, name):
+    batch = W.random_small(3) if name == "r3" else getattr(W, name)()
+    run = _Flow("gqa_quest_sparse_attention", batch, gpu)
+    run.step()
+    torch.cuda.synchronize()
+    f, ic = run.flow, run.ic
+    # the envelopes the cache side wrote for the closed pages
+    cmax, rows = O.page_reduce(_bits(run.k), np.zeros_like(_bits(run.cache["max"])), _np(run.loc),
+                               batch.num_kv_heads, batch.page_size, 1, O.MAX)
+    np.testing.assert_array_equal(_bits(run.cache["max"])[rows], cmax[rows])
+    dense, wi = _np(ic.dense_kv_indices), _owinfo(ic)
+    s_max, cov = O.ragged_binary(O.BINARY_MUL, 1.0, 1.0, _bits(run.q), O.ROWS_BATCHED, _bits(run.cache["max"]),
+                                 O.ROWS_PAGED, _bits(f.mul_max.output_buffer), dense, *wi)
+    np.testing.assert_array_equal(_bits(f.mul_max.output_buffer), s_max)
+    s = _bits(f.maximum_op.output_buffer)
+    exp_s, _ = O.ragged_binary(O.BINARY_MAXIMUM, 1.0, 1.0, _bits(f.mul_max.output_buffer), O.ROWS_RAGGED,
+                               _bits(f.mul_min.output_buffer), O.ROWS_RAGGED, s, dense, *wi)
+    np.testing.assert_array_equal(s, exp_s)
+    score = _bits(f.sum.output_buffer)
+    exp_score, _ = O.ragged_reduce(s, score, 2, O.REDUCE_SUM, *wi[1:])
+    np.testing.assert_allclose(_f(score[cov]), _f(exp_score[cov]), rtol=1e-2, atol=1e-3)
+    aggr = _bits(f.max_op.output_buffer)
+    exp_aggr, _ = O.ragged_reduce(score, aggr, 1, O.MAX, *wi[1:])
+    np.testing.assert_array_equal(aggr[cov], exp_aggr[cov])
+    _check_selection(run, aggr)
+
+
+@pytest.mark.parametrize("flow_name", ["gqa_block_sparse_attention", "gqa_quest_sparse_attention"])
+def test_flow_graph_replay_matches_eager(gpu, flow_name):
+    run = _Flow(flow_name, W.c2(), gpu)
+    run.step()
+    torch.cuda.synchronize()
+    eager = run.ic.sparse_kv_indices.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run.step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        run.step()
+    for _ in range(4):
+        run.ic.sparse_kv_indices.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(run.ic.sparse_kv_indices, eager)

@@ -56,11 +56,35 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
+    "vtx_ragged_gemm": (
+        [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
+         _vp, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_ragged_binary": (
+        [_i32, ctypes.c_float, ctypes.c_float, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _i32, _i32, _i32,
+         _vp, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_ragged_unary": (
+        [_i32, ctypes.c_float, ctypes.c_float, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _vp, _i64, _vp, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_ragged_reduce": (
+        [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _i64, _vp, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_segment_scan": (
+        [_i32, ctypes.c_float, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
-REDUCE_MEAN, REDUCE_MAX, REDUCE_MIN, REDUCE_L2NORM = 0, 1, 2, 3
+REDUCE_MEAN, REDUCE_MAX, REDUCE_MIN, REDUCE_L2NORM, REDUCE_SUM = 0, 1, 2, 3, 4
+ROWS_BATCHED, ROWS_PAGED, ROWS_RAGGED = 0, 1, 2
+SEGMENT_SOFTMAX, SEGMENT_NORMALIZE = 0, 1
 DTYPE_BF16, DTYPE_F32 = 0, 1
 FUSED_AUTO, FUSED_SEGMENT, FUSED_SPLIT = 0, 1, 2
 
@@ -448,3 +472,115 @@ def indexer_fused(
             seg_counters.numel() if seg_counters is not None else 0, int(mode),
             _stream(dev))
     _check(rc, "indexer_fused")
+
+
+# ----------------------------------------------------------------------------
+# workload-walking indexer ops (GQA / Quest flows)
+# ----------------------------------------------------------------------------
+def _tile(t: torch.Tensor, name: str):
+    """(rows, d0, d1) of a rank-3 (or rank-2 as [rows, 1, d1]) bf16 tensor."""
+    _req(t, torch.bfloat16, name)
+    if t.dim() == 3:
+        return int(t.shape[0]), int(t.shape[1]), int(t.shape[2])
+    if t.dim() == 2:
+        return int(t.shape[0]), 1, int(t.shape[1])
+    raise RuntimeError(f"vortex_torch: {name} must be rank 3 [rows, d0, d1]")
+
+
+def _walk_args(winfo, dense=None):
+    """Device pointers and capacity of a workload list (q, off, len, num)."""
+    wq, woff, wlen, wnum = winfo
+    for t, n in ((woff, "winfo_kv_offsets"), (wlen, "winfo_kv_lens"), (wnum, "winfo_num_workloads")):
+        _req(t, torch.int32, n)
+    if wq is not None:
+        _req(wq, torch.int32, "winfo_q_indices")
+    if dense is not None:
+        _req(dense, torch.int32, "dense_kv_indices")
+    cap = min(woff.numel(), wlen.numel(), *( [wq.numel()] if wq is not None else []))
+    return (wq.data_ptr() if wq is not None else None, woff.data_ptr(), wlen.data_ptr(), cap, wnum.data_ptr())
+
+
+@_plain_args
+def ragged_gemm(x, x_mode: int, y, y_mode: int, o, dense_kv_indices, winfo) -> None:
+    """o[p, c, g] = sum_k x[rx, g, k] * y[ry, c, k] over the workload list
+    winfo = (winfo_q_indices, winfo_kv_offsets, winfo_kv_lens, winfo_num_workloads)."""
+    lib = load_library()
+    dev = _require_gpu(x, y, o, dense_kv_indices, *[t for t in winfo if t is not None])
+    xr, G, K = _tile(x, "x")
+    yr, C, Ky = _tile(y, "y")
+    orows, oc, og = _tile(o, "o")
+    if K != Ky:
+        raise RuntimeError(f"vortex_torch: GeMM inner dimension mismatch ({K} vs {Ky})")
+    if oc * og != C * G:
+        raise RuntimeError(f"vortex_torch: GeMM output tile must be [{C}, {G}], got [{oc}, {og}]")
+    wq, woff, wlen, cap, wnum = _walk_args(winfo, dense_kv_indices)
+    with _on_device(dev):
+        rc = lib.vtx_ragged_gemm(x.data_ptr(), xr, int(x_mode), G, y.data_ptr(), yr, int(y_mode), C, K,
+                                 o.data_ptr(), orows, dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+                                 wq, woff, wlen, cap, wnum, _stream(dev))
+    _check(rc, "ragged_gemm")
+
+
+@_plain_args
+def ragged_binary(op: int, alpha: float, beta: float, x, x_mode: int, y, y_mode: int, o,
+                  dense_kv_indices, winfo) -> None:
+    """o[p] = op(x[rx], y[ry]) with broadcasting over size-1 tile axes."""
+    lib = load_library()
+    dev = _require_gpu(x, y, o, dense_kv_indices, *[t for t in winfo if t is not None])
+    xr, x0, x1 = _tile(x, "x")
+    yr, y0, y1 = _tile(y, "y")
+    orows, o0, o1 = _tile(o, "o")
+    wq, woff, wlen, cap, wnum = _walk_args(winfo, dense_kv_indices)
+    with _on_device(dev):
+        rc = lib.vtx_ragged_binary(int(op), float(alpha), float(beta), x.data_ptr(), xr, int(x_mode), x0, x1,
+                                   y.data_ptr(), yr, int(y_mode), y0, y1, o.data_ptr(), orows, o0, o1,
+                                   dense_kv_indices.data_ptr(), dense_kv_indices.numel(), wq, woff, wlen, cap,
+                                   wnum, _stream(dev))
+    _check(rc, "ragged_binary")
+
+
+@_plain_args
+def ragged_unary(op: int, alpha: float, beta: float, x, o, winfo) -> None:
+    lib = load_library()
+    dev = _require_gpu(x, o, *[t for t in winfo if t is not None])
+    xr, d0, d1 = _tile(x, "x")
+    orows, o0, o1 = _tile(o, "o")
+    if (o0, o1) != (d0, d1):
+        raise RuntimeError("vortex_torch: elementwise output tile must equal the input tile")
+    _, woff, wlen, cap, wnum = _walk_args((None,) + tuple(winfo[1:]))
+    with _on_device(dev):
+        rc = lib.vtx_ragged_unary(int(op), float(alpha), float(beta), x.data_ptr(), xr, d0, d1, o.data_ptr(), orows,
+                                  woff, wlen, cap, wnum, _stream(dev))
+    _check(rc, "ragged_unary")
+
+
+@_plain_args
+def ragged_reduce(x, o, dim: int, reduce_type: int, winfo) -> None:
+    lib = load_library()
+    dev = _require_gpu(x, o, *[t for t in winfo if t is not None])
+    xr, d0, d1 = _tile(x, "x")
+    _req(o, torch.bfloat16, "o")
+    per = d1 if int(dim) == 1 else d0
+    _, woff, wlen, cap, wnum = _walk_args((None,) + tuple(winfo[1:]))
+    with _on_device(dev):
+        rc = lib.vtx_ragged_reduce(x.data_ptr(), xr, d0, d1, o.data_ptr(), o.numel() // max(per, 1), int(dim),
+                                   int(reduce_type), woff, wlen, cap, wnum, _stream(dev))
+    _check(rc, "ragged_reduce")
+
+
+@_plain_args
+def segment_scan(op: int, scale: float, x, dense_kv_indptr, eff_batch_size: int, topk_val: int,
+                 reserved_bos: int, reserved_eos: int) -> None:
+    """In-place segment softmax (op SEGMENT_SOFTMAX) or L2 normalize over each
+    segment's middle positions, per tile column."""
+    lib = load_library()
+    dev = _require_gpu(x, dense_kv_indptr)
+    xr, d0, d1 = _tile(x, "x")
+    _req(dense_kv_indptr, torch.int32, "dense_kv_indptr")
+    eff = int(eff_batch_size)
+    if dense_kv_indptr.numel() < eff + 1:
+        raise RuntimeError(f"vortex_torch: dense_kv_indptr needs {eff + 1} entries")
+    with _on_device(dev):
+        rc = lib.vtx_segment_scan(int(op), float(scale), x.data_ptr(), xr, d0 * d1, dense_kv_indptr.data_ptr(), eff,
+                                  int(topk_val), int(reserved_bos), int(reserved_eos), _stream(dev))
+    _check(rc, "segment_scan")

@@ -21,6 +21,7 @@ import torch
 
 from .. import _deferred, _hip
 from ..abs import FORMAT, as_vtensor, vOp, vTensor
+from . import _walk
 from .context import Context
 
 
@@ -153,4 +154,66 @@ class GeMV(vOp):
         return self.output_buffer
 
 
-__all__ = ["GeMV", "mv_bpr"]
+def _mm(x_fmt: FORMAT, y_fmt: FORMAT) -> Callable:
+    def impl(x: torch.Tensor, y: torch.Tensor, o: torch.Tensor, ctx: Context) -> None:
+        _walk.ready(x, y)
+        _hip.ragged_gemm(x, _walk.ROW_MODE[x_fmt], y, _walk.ROW_MODE[y_fmt], o, ctx.dense_kv_indices,
+                         _walk.winfo(ctx))
+    return impl
+
+
+#: o[p] = y[p] x[p]^T ([C, G] per position) over ctx's workload list
+#: (reference indexer/triton_kernels/matmul_impl.py: mm_bpr 6-113, mm_rrr and mm_rpr 127-391).
+mm_bpr = _mm(FORMAT.BATCHED, FORMAT.PAGED)
+mm_rrr = _mm(FORMAT.RAGGED, FORMAT.RAGGED)
+mm_rpr = _mm(FORMAT.RAGGED, FORMAT.PAGED)
+
+
+class GeMM(vOp):
+    """O[s] = Y[s] X[s]^T per packed position: x [B or S, N_x, K], y [S, N_y, K]
+    -> RAGGED [ctx.max_num_pages, N_y, N_x] (reference vortex_torch/indexer/matmul.py:193-398)."""
+
+    _impl_map: Dict[Tuple[FORMAT, FORMAT], Tuple[Callable, FORMAT]] = {
+        (FORMAT.BATCHED, FORMAT.PAGED): (mm_bpr, FORMAT.RAGGED),
+        (FORMAT.RAGGED, FORMAT.RAGGED): (mm_rrr, FORMAT.RAGGED),
+        (FORMAT.RAGGED, FORMAT.PAGED): (mm_rpr, FORMAT.RAGGED),
+    }
+
+    def __init__(self):
+        super().__init__()
+        self.impl: Optional[Callable] = None
+        self.output_format: Optional[FORMAT] = None
+        self.output_buffer: Optional[torch.Tensor] = None
+
+    def profile(self, x: vTensor, y: vTensor, ctx: Context) -> vTensor:
+        p = self._prefix()
+        assert isinstance(x, vTensor), f"{p}profile expects x to be vTensor, got {type(x)}"
+        assert isinstance(y, vTensor), f"{p}profile expects y to be vTensor, got {type(y)}"
+        assert x.dim() == 3 and y.dim() == 3, (
+            f"{p}expected 3D inputs; got x.ndim={x.dim()}, y.ndim={y.dim()}")
+        assert x.shape[2] == y.shape[2], (
+            f"{p}last dimension mismatch: x.shape[2]={x.shape[2]} vs y.shape[2]={y.shape[2]}")
+        key = (x._format, y._format)
+        assert key in self._impl_map, (
+            f"{p}no implementation for (x_fmt={key[0]}, y_fmt={key[1]}). "
+            f"Available: {list(self._impl_map.keys())}")
+        self.impl, self.output_format = self._impl_map[key]
+        Ny, Nx = y.shape[1], x.shape[1]
+        self.output_buffer = torch.empty((ctx.max_num_pages, Ny, Nx), device=x.device, dtype=x.dtype)
+        ctx.add_aux_memory(self.output_buffer)
+        for t in (x, y):
+            if t._format == FORMAT.PAGED:
+                ctx.add_aux_flops(t.shape[1] * t.shape[2])
+        return as_vtensor(self.output_buffer, self.output_format)
+
+    def execute(self, x: torch.Tensor, y: torch.Tensor, ctx: Context) -> torch.Tensor:
+        p = self._prefix()
+        assert self.impl is not None, f"{p}execute called before profile() (impl is None)"
+        assert self.output_buffer is not None, f"{p}output buffer is None; did profile() run?"
+        assert x.device == y.device == self.output_buffer.device, (
+            f"{p}device mismatch: x={x.device}, y={y.device}, o={self.output_buffer.device}")
+        self.impl(x, y, self.output_buffer, ctx)
+        return self.output_buffer
+
+
+__all__ = ["GeMV", "GeMM", "mv_bpr", "mm_bpr", "mm_rrr", "mm_rpr"]
