@@ -327,6 +327,21 @@ int vtx_segment_scan(int32_t op, float scale, uint16_t* x, int64_t x_rows, int32
                      const int32_t* dense_kv_indptr, int32_t eff_batch_size, int32_t topk_val,
                      int32_t reserved_bos, int32_t reserved_eos, void* stream);
 
+/*
+ * Writes new keys and values into the paged pools: for token i < nnz and
+ * kv head h, with pos = loc[i], pool row
+ *   (pos / page_size) * (page_size * H) + h * page_size + pos % page_size
+ * of k_cache / v_cache ([cache_rows, head_dim] elements of elem_bytes each,
+ * i.e. [pages * H, page_size, head_dim]) receives new_k[i, h, :] /
+ * new_v[i, h, :] ([nnz, H, head_dim]).  Raw element copy; tokens whose row
+ * is outside the pool are skipped.
+ * Replaces set_kv_buffer_launcher / set_kv_buffer_kernel (reference
+ * vortex_torch/cache/triton_kernels/set_kv.py:5-63).
+ */
+int vtx_set_kv_buffer(void* k_cache, void* v_cache, int64_t cache_rows, const void* new_k,
+                      const void* new_v, const int64_t* loc, int64_t nnz, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t elem_bytes, int32_t page_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -460,3 +460,28 @@ def segment_scan(op: int, scale: float, x_bits, dense_indptr, eff_batch_size: in
         flat[a:b] = f32_to_bf16(r.astype(np.float32))
         touched[a:b] = True
     return out, touched
+
+
+# --------------------------------------------------------------------------
+# A.6 set_kv_buffer — cache/triton_kernels/set_kv.py:5-63
+# --------------------------------------------------------------------------
+
+
+def set_kv_buffer(k_cache, v_cache, new_k, new_v, loc, page_size: int):
+    """Returns copies of the pools with token i / head h written at pool row
+    (loc // P) * (P * H) + h * P + loc % P (C division), rows outside the
+    pool skipped.  Pools [rows, P, D] are viewed as [rows * P, D]."""
+    k = np.array(k_cache, copy=True)
+    v = np.array(v_cache, copy=True)
+    kf = k.reshape(-1, k.shape[-1])
+    vf = v.reshape(-1, v.shape[-1])
+    nk = np.asarray(new_k)
+    nv = np.asarray(new_v)
+    nnz, H = nk.shape[0], nk.shape[1]
+    pos = np.asarray(loc, dtype=np.int64)[:nnz]
+    for h in range(H):
+        dst = c_div(pos, page_size) * (page_size * H) + h * page_size + c_mod(pos, page_size)
+        ok = (pos >= 0) & (dst < kf.shape[0])
+        kf[dst[ok]] = nk[ok, h]
+        vf[dst[ok]] = nv[ok, h]
+    return k, v

@@ -291,3 +291,60 @@ def test_flow_graph_replay_matches_eager(gpu, flow_name):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(run.ic.sparse_kv_indices, eager)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 100),
+                                     (torch.bfloat16, 3), (torch.bfloat16, 576)])
+@pytest.mark.parametrize("kind", ["decode", "prefill"])
+def test_set_kv_buffer_matches_oracle(gpu, dtype, D, kind):
+    from vortex_torch.cache import set_kv_buffer_launcher
+
+    P, H, pages = 16, 8 if D != 576 else 1, 300
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn((pages * H, P, D), generator=g).to(dtype)
+    v = torch.randn((pages * H, P, D), generator=g).to(dtype)
+    if kind == "decode":
+        loc = torch.randperm(pages * P, generator=g)[:64].to(torch.int64)
+    else:  # every slot of 40 pages, shuffled, plus two tokens outside the pool
+        pg = torch.randperm(pages, generator=g)[:40]
+        loc = (pg[:, None] * P + torch.arange(P)).reshape(-1)
+        loc = torch.cat([loc[torch.randperm(loc.numel(), generator=g)], torch.tensor([-3, pages * P + 1])])
+    nk = torch.randn((loc.numel(), H, D), generator=g).to(dtype)
+    nv = torch.randn((loc.numel(), H, D), generator=g).to(dtype)
+    bits = (lambda t: t.view(torch.int16).numpy()) if dtype == torch.bfloat16 else (lambda t: t.view(torch.int32).numpy())
+    ek, ev = O.set_kv_buffer(bits(k), bits(v), bits(nk), bits(nv), loc.numpy(), P)
+    kd, vd = k.to(gpu), v.to(gpu)
+    set_kv_buffer_launcher(kd, vd, nk.to(gpu), nv.to(gpu), loc.to(gpu), P)
+    np.testing.assert_array_equal(bits(kd.cpu()), ek)
+    np.testing.assert_array_equal(bits(vd.cpu()), ev)
+
+
+def test_set_kv_then_cmean(gpu):
+    """Decode step on the cache side: the new tokens go into the pool, then
+    CMean of the pages they close equals the oracle's mean of the new pool."""
+    from vortex_torch.cache import Mean as CMean, set_kv_buffer_launcher
+
+    batch = W.c2()
+    ic, cc = W.make_contexts(batch, gpu)
+    H, D, P = batch.num_kv_heads, batch.head_dim, batch.page_size
+    k = W.randn_bf16((batch.pool_pages * H, P, D), 1, gpu)
+    v = torch.zeros_like(k)
+    loc = W.decode_loc(batch).to(gpu)
+    nk = W.randn_bf16((loc.numel(), H, D), 2, gpu)
+    set_kv_buffer_launcher(k, v, nk, nk, loc, P)
+    cen = torch.zeros((batch.pool_pages * H, 1, D), device=gpu, dtype=torch.bfloat16)
+    op = CMean(dim=1)
+    cc.profile()
+    op(as_vtensor(k, FORMAT.PAGED), as_vtensor(cen, FORMAT.PAGED), loc=loc, ctx=cc)
+    cc.execute()
+    op(as_vtensor(k, FORMAT.PAGED), as_vtensor(cen, FORMAT.PAGED), loc=loc, ctx=cc)
+    torch.cuda.synchronize()
+    exp, rows = O.page_reduce(_bits(k), np.zeros_like(_bits(cen)), _np(loc), H, P, 1, O.MEAN)
+    assert rows.size > 0
+    np.testing.assert_allclose(_f(_bits(cen)[rows]), _f(exp[rows]), rtol=1e-2, atol=1e-3)
+    # the written slots hold the new tokens
+    pos = _np(loc)
+    for i in range(0, loc.numel(), 9):
+        for h in (0, H - 1):
+            got = k[(int(pos[i]) // P) * H + h, int(pos[i]) % P]
+            assert torch.equal(got, nk[i, h])

@@ -232,3 +232,27 @@ def test_segment_softmax_closed_form():
         if n > 4:
             a, b = int(dip[s]) + 1, int(dip[s + 1]) - 1
             assert (got[a:b].reshape(-1) == O.f32_to_bf16(np.float32(1.0 / (b - a))).reshape(-1)[0]).all()
+
+
+def test_set_kv_buffer_against_loops():
+    rng = np.random.default_rng(3)
+    P, H, D, pages = 4, 3, 5, 6
+    k = rng.integers(0, 1000, size=(pages * H, P, D)).astype(np.uint16)
+    v = rng.integers(0, 1000, size=(pages * H, P, D)).astype(np.uint16)
+    nnz = 9
+    nk = rng.integers(0, 1000, size=(nnz, H, D)).astype(np.uint16)
+    nv = rng.integers(0, 1000, size=(nnz, H, D)).astype(np.uint16)
+    loc = rng.permutation(pages * P)[:nnz].astype(np.int64)
+    loc[2] = -5              # skipped
+    loc[5] = pages * P + 3   # past the pool: skipped
+    gk, gv = O.set_kv_buffer(k, v, nk, nv, loc, P)
+    ek, ev = k.copy(), v.copy()
+    for i in range(nnz):
+        pos = int(loc[i])
+        if pos < 0 or pos >= pages * P:
+            continue
+        for h in range(H):
+            ek[(pos // P) * H + h, pos % P] = nk[i, h]   # pool row page*H + h, slot pos % P
+            ev[(pos // P) * H + h, pos % P] = nv[i, h]
+    np.testing.assert_array_equal(gk, ek)
+    np.testing.assert_array_equal(gv, ev)

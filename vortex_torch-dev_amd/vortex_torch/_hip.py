@@ -74,6 +74,10 @@ _SIGNATURES = {
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _i64, _vp, _vp],
         ctypes.c_int,
     ),
+    "vtx_set_kv_buffer": (
+        [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
     "vtx_segment_scan": (
         [_i32, ctypes.c_float, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
@@ -584,3 +588,29 @@ def segment_scan(op: int, scale: float, x, dense_kv_indptr, eff_batch_size: int,
         rc = lib.vtx_segment_scan(int(op), float(scale), x.data_ptr(), xr, d0 * d1, dense_kv_indptr.data_ptr(), eff,
                                   int(topk_val), int(reserved_bos), int(reserved_eos), _stream(dev))
     _check(rc, "segment_scan")
+
+
+@_plain_args
+def set_kv_buffer(k_cache, v_cache, new_k, new_v, loc, page_size: int) -> None:
+    """Writes new_k / new_v [nnz, H, D] into the paged pools at the token
+    slots loc (int64 [nnz]); pools [pages * H, page_size, D] of the same dtype."""
+    lib = load_library()
+    dev = _require_gpu(k_cache, v_cache, new_k, new_v, loc)
+    _req(loc, torch.int64, "loc")
+    if new_k.dim() != 3 or new_v.shape != new_k.shape:
+        raise RuntimeError("vortex_torch: new_k and new_v must both be [nnz, num_kv_heads, head_dim]")
+    for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache"), (new_k, "new_k"), (new_v, "new_v")):
+        if t.dtype != new_k.dtype:
+            raise RuntimeError(f"vortex_torch: {n} is {t.dtype}, the new tokens are {new_k.dtype}")
+        if not t.is_contiguous():
+            raise RuntimeError(f"vortex_torch: {n} must be contiguous")
+    nnz, H, D = (int(s) for s in new_k.shape)
+    if loc.numel() < nnz:
+        raise RuntimeError("vortex_torch: loc shorter than the new tokens")
+    if k_cache.shape != v_cache.shape or int(k_cache.shape[-1]) != D:
+        raise RuntimeError("vortex_torch: k_cache and v_cache must be [pages * H, page_size, head_dim]")
+    with _on_device(dev):
+        rc = lib.vtx_set_kv_buffer(k_cache.data_ptr(), v_cache.data_ptr(), k_cache.numel() // D, new_k.data_ptr(),
+                                   new_v.data_ptr(), loc.data_ptr(), nnz, H, D, new_k.element_size(),
+                                   int(page_size), _stream(dev))
+    _check(rc, "set_kv_buffer")
