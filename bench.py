@@ -26,8 +26,12 @@ Other configurations (side measurements, not the headline):
                      known size), and exits: the program a counter pass
                      (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) profiles.
 
+  --flow gqa / quest the same decode step with gqa_block_sparse_attention or
+                     gqa_quest_sparse_attention (every op launched on its own).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--config c2|c3|c4|c5] [--layers N] [--traffic-probe]
+                       [--config c2|c3|c4|c5] [--flow block_sparse|gqa|quest]
+                       [--layers N] [--traffic-probe]
 """
 from __future__ import annotations
 
@@ -67,10 +71,15 @@ def _parse():
     ap.add_argument("--no-unfused", action="store_true", help="skip the unfused comparison")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
+    ap.add_argument("--flow", default="block_sparse", choices=sorted(FLOWS),
+                    help="registered flow of the decode step (side measurement unless block_sparse)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the kernels a counter pass profiles, print their sizes, exit")
     return ap.parse_args()
 
+
+FLOWS = {"block_sparse": "block_sparse_attention", "gqa": "gqa_block_sparse_attention",
+         "quest": "gqa_quest_sparse_attention"}
 
 DECODE_CONFIGS = {
     "c2": ("C2: decode step, batch 64, L~U[1024,8192], 27 sparse layers, Qwen3-1.7B head shape "
@@ -105,7 +114,8 @@ def fused_kernel_name(batch: W.DecodeBatch) -> str:
 class DecodeStep:
     """All device state of one C2 decode step, built through the public API."""
 
-    def __init__(self, batch: W.DecodeBatch, layers: int, dev: torch.device, seed: int = 7):
+    def __init__(self, batch: W.DecodeBatch, layers: int, dev: torch.device, seed: int = 7,
+                 flow_name: str = "block_sparse_attention"):
         from vortex_torch import flow as vflow
         from vortex_torch.abs import FORMAT, as_vtensor
 
@@ -121,13 +131,17 @@ class DecodeStep:
         self.plain = []  # (k, centroids, q) without the layout tag
         rows = batch.pool_pages * H
         for layer in range(layers):
-            f = vflow.build_vflow("block_sparse_attention")
+            f = vflow.build_vflow(flow_name)
             k = W.randn_bf16((rows, P, D), seed + 3 * layer, dev)
-            cen = W.randn_bf16((rows, 1, D), seed + 3 * layer + 1, dev, std=0.25)
             qp = W.randn_bf16((B * H, G, D), seed + 3 * layer + 2, dev)
+            cache = {"k": as_vtensor(k, FORMAT.PAGED)}
+            for j, (name, (r, c)) in enumerate(f.create_cache(P, D).items()):
+                cache[name] = as_vtensor(W.randn_bf16((rows, r, c), seed + 3 * layer + 1 + 101 * j, dev, std=0.25),
+                                         FORMAT.PAGED)
+            cen = cache.get("centroids")
             self.plain.append((k, cen, qp))
             self.flows.append(f)
-            self.caches.append({"k": as_vtensor(k, FORMAT.PAGED), "centroids": as_vtensor(cen, FORMAT.PAGED)})
+            self.caches.append(cache)
             self.qs.append(as_vtensor(qp, FORMAT.BATCHED))
         self.o = as_vtensor(self.ictx.sparse_kv_indices.view(-1, 1, 1), FORMAT.RAGGED)
 
@@ -358,6 +372,37 @@ def bench_decode(args, dev) -> dict:
     return out
 
 
+def bench_flow(args, dev) -> dict:
+    """Side measurement: the decode step of another registered flow (every
+    op launched on its own, one HIP graph per step)."""
+    batch = getattr(W, args.config)()
+    name = FLOWS[args.flow]
+    print(f"[bench] building {args.config.upper()} step of {name}: {batch.batch} requests, {args.layers} layers",
+          file=sys.stderr, flush=True)
+    step = DecodeStep(batch, args.layers, dev, flow_name=name)
+    g = capture(step.run)
+    us_step = time_graph(g, args.steps, args.warmup) * 1000.0
+    plan = plan_summary(step)
+    H, G, D, B = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.batch
+    covered = int(plan["winfo_len"].sum())
+    seg_n = np.diff(plan["dense_indptr"].astype(np.int64)) - batch.bos - batch.eos
+    sel = int((seg_n > batch.topk).sum()) * batch.topk * 4
+    rows_per_page = 2 if args.flow == "quest" else 1  # envelopes max + min, or one centroid
+    per_layer = B * H * G * D * 2 + covered * (rows_per_page * 2 * D + 4 + 2) + sel
+    gbps = per_layer * args.layers / (us_step * 1e-6) / 1e9
+    print(f"[bench] {name} step {us_step:.1f} us", file=sys.stderr, flush=True)
+    return {
+        "metric": f"us per decode step of {name} (indexer + cache), side measurement",
+        "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(us_step / 1000.0, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded)",
+        "config": {"workload": f"{DECODE_CONFIGS[args.config]}; flow {name}", "layers": args.layers},
+        "min_bytes_per_layer": per_layer,
+        "achieved_GBps_of_min_bytes": round(gbps, 1),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+    }
+
+
 def traffic_probe(step: DecodeStep, dev) -> dict:
     """Kernels for a counter pass: every layer's fused indexer launch (twice:
     the second pass is the one to read, the first warms the code object and
@@ -465,7 +510,12 @@ def main():
     _hip.load_library()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    out = bench_burst(args, dev) if args.config == "c4" else bench_decode(args, dev)
+    if args.config == "c4":
+        out = bench_burst(args, dev)
+    elif args.flow != "block_sparse":
+        out = bench_flow(args, dev)
+    else:
+        out = bench_decode(args, dev)
     print(json.dumps(out), flush=True)
 
 

@@ -80,6 +80,39 @@ int vtx_plan_decode(const int32_t* cached_seq_lens, int32_t batch_size,
                     void* stream);
 
 /*
+ * FA3 variant of the decode planner: the block tables, indptrs and workload
+ * list of vtx_plan_decode (kv_last_page_len is not an output), plus, for
+ * every segment s = b*H + h < page_table_rows:
+ *   dense_page_table[s * page_table_stride + j]  = dense index of page j
+ *   sparse_page_table[s * page_table_stride + i] = sparse_kv_indices entry i
+ *        for the entries the planner writes (all pages when n_b <= budget,
+ *        else the BOS and EOS slots; the top-k slots are left untouched)
+ * (entries past page_table_stride are not written), and for s < cache_seqlens_len:
+ *   dense_cache_seqlens[s]  = cached_seq_lens[b]
+ *   sparse_cache_seqlens[s] = min((budget - 1) * page_size + last_page_len,
+ *                                 cached_seq_lens[b])
+ * Replaces sglang_plan_decode_fa3 (reference csrc/utils_sglang.cu:1085-1239,
+ * kernels 950-1082), bound at vortex_torch/indexer/utils_sglang.py:135-168.
+ * One launch; no limit on batch_size (reference: 1024 requests, 8192 segments).
+ */
+int vtx_plan_decode_fa3(const int32_t* cached_seq_lens, int32_t batch_size,
+                        int32_t* dense_kv_indptr, int32_t* dense_kv_indices,
+                        int64_t dense_kv_indices_len, int32_t* sparse_kv_indptr,
+                        int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                        int32_t* dense_page_table, int32_t* dense_cache_seqlens,
+                        int32_t* sparse_page_table, int32_t* sparse_cache_seqlens,
+                        int64_t page_table_rows, int64_t page_table_stride,
+                        int64_t cache_seqlens_len, const int32_t* req_to_token,
+                        int64_t req_to_token_rows, int64_t req_to_token_stride,
+                        const int64_t* req_indices, int32_t* winfo_q_indices,
+                        int32_t* winfo_kv_offsets, int32_t* winfo_kv_lens,
+                        int64_t winfo_capacity, int32_t* winfo_num_workloads,
+                        int32_t* winfo_chunk_size, int32_t page_size, int32_t num_kv_heads,
+                        int32_t topk_val, int32_t page_reserved_bos,
+                        int32_t page_reserved_eos, int32_t max_chunk_size,
+                        int32_t min_chunk_size, void* stream);
+
+/*
  * Paged GeMV scorer: for every workload w < *winfo_num_workloads and every
  * t < winfo_kv_lens[w], with p = winfo_kv_offsets[w] + t:
  *     o[p] = bf16( sum_d float(x[winfo_q_indices[w], d]) *

@@ -485,3 +485,46 @@ def set_kv_buffer(k_cache, v_cache, new_k, new_v, loc, page_size: int):
         kf[dst[ok]] = nk[ok, h]
         vf[dst[ok]] = nv[ok, h]
     return k, v
+
+
+# --------------------------------------------------------------------------
+# A.7 FA3 decode planner — csrc/utils_sglang.cu:950-1082 (host 1085-1239)
+# --------------------------------------------------------------------------
+
+
+def plan_decode_fa3(seq_lens, req_to_token, req_indices, page_size: int, num_kv_heads: int, topk_val: int,
+                    bos: int, eos: int, max_chunk_size: int, page_table_stride: int) -> dict:
+    """plan_decode's block tables and workload list (the FA3 planner writes no
+    kv_last_page_len) plus, per segment s = b*H + h:
+      dense_page_table[s, j]  = dense index of page j (j < stride)
+      sparse_page_table[s, i] = sparse entry i where the planner writes it
+                                (masks *_pt_written say which entries)
+      dense_cache_seqlens[s]  = L_b
+      sparse_cache_seqlens[s] = min((budget - 1) * P + last_page_len, L_b)
+    (utils_sglang.cu:966-977 for the lengths, 1041-1078 for the tables)."""
+    r = plan_decode(seq_lens, req_to_token, req_indices, page_size, num_kv_heads, topk_val, bos, eos,
+                    max_chunk_size)
+    L = np.asarray(seq_lens, dtype=np.int64)
+    H, P, W = int(num_kv_heads), int(page_size), int(page_table_stride)
+    S = L.shape[0] * H
+    budget = topk_val + bos + eos
+    dip, sip = r["dense_indptr"].astype(np.int64), r["sparse_indptr"].astype(np.int64)
+    dpt = np.zeros((S, W), np.int32)
+    spt = np.zeros((S, W), np.int32)
+    dpt_w = np.zeros((S, W), bool)
+    spt_w = np.zeros((S, W), bool)
+    for s in range(S):
+        k = min(int(dip[s + 1] - dip[s]), W)
+        dpt[s, :k] = r["dense_indices"][dip[s]:dip[s] + k]
+        dpt_w[s, :k] = True
+        m = min(int(sip[s + 1] - sip[s]), W)
+        w = r["sparse_written"][sip[s]:sip[s] + m]
+        spt[s, :m][w] = r["sparse_indices"][sip[s]:sip[s] + m][w]
+        spt_w[s, :m] = w
+    last = r["kv_last_page_len"].astype(np.int64)
+    dcs = np.repeat(L, H)
+    scs = np.minimum((budget - 1) * P + last, dcs)
+    r.update({"dense_page_table": dpt, "sparse_page_table": spt, "dense_pt_written": dpt_w,
+              "sparse_pt_written": spt_w, "dense_cache_seqlens": dcs.astype(np.int32),
+              "sparse_cache_seqlens": scs.astype(np.int32)})
+    return r

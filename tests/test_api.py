@@ -280,7 +280,9 @@ def test_out_of_scope_entry_points_say_so():
     with pytest.raises(NotImplementedError, match="prefill"):
         vortex_torch_C.sglang_plan_prefill()
     with pytest.raises(NotImplementedError):
-        utils_sglang.plan_decode_fa3()
+        utils_sglang.plan_prefill_fa3()
+    with pytest.raises(NotImplementedError, match="prefill"):
+        vortex_torch_C.Chunkwise_HN2NH_Transpose_FA3()
     assert utils_sglang.indices_to_page_table(None, None) is None
 
 

@@ -348,3 +348,46 @@ def test_set_kv_then_cmean(gpu):
         for h in (0, H - 1):
             got = k[(int(pos[i]) // P) * H + h, int(pos[i]) % P]
             assert torch.equal(got, nk[i, h])
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c5", "r1", "r2", "r8", "r13"])
+def test_plan_decode_fa3_matches_oracle(gpu, name):
+    """FA3 planner through utils_sglang.plan_decode_fa3: every output bit-exact
+    against the oracle; table entries the planner does not write keep their
+    sentinel; kv_last_page_len is not an output."""
+    from vortex_torch.indexer.utils_sglang import plan_decode_fa3
+
+    batch = W.random_small(int(name[1:])) if name.startswith("r") else getattr(W, name)()
+    ic, _ = W.make_contexts(batch, gpu)
+    ic.kv_last_page_len.fill_(-9)
+    S = max(1, batch.batch * batch.num_kv_heads)
+    stride = batch.max_pages_per_request
+    i32 = dict(dtype=torch.int32, device=gpu)
+    dpt, spt = torch.full((S, stride), -5, **i32), torch.full((S, stride), -5, **i32)
+    dcs, scs = torch.full((S,), -5, **i32), torch.full((S,), -5, **i32)
+    b = batch.to(gpu)
+    plan_decode_fa3(b.seq_lens, b.req_to_token, b.req_indices, dpt, dcs, spt, scs, ic)
+    ref = O.plan_decode_fa3(batch.seq_lens.numpy(), batch.req_to_token.numpy(), batch.req_indices.numpy(),
+                            batch.page_size, batch.num_kv_heads, batch.topk, batch.bos, batch.eos, batch.max_chunk,
+                            stride)
+    n = batch.batch * batch.num_kv_heads
+    np.testing.assert_array_equal(_np(ic.dense_kv_indptr)[:n + 1], ref["dense_indptr"])
+    np.testing.assert_array_equal(_np(ic.sparse_kv_indptr)[:n + 1], ref["sparse_indptr"])
+    nd = ref["dense_indices"].size
+    np.testing.assert_array_equal(_np(ic.dense_kv_indices)[:nd], ref["dense_indices"])
+    w = ref["sparse_written"]
+    np.testing.assert_array_equal(_np(ic.sparse_kv_indices)[:w.size][w], ref["sparse_indices"][w])
+    nw = ref["num_workloads"]
+    assert int(ic.winfo_num_workloads.item()) == nw
+    np.testing.assert_array_equal(_np(ic.winfo_kv_offsets)[:nw], ref["winfo_off"])
+    np.testing.assert_array_equal(_np(ic.winfo_kv_lens)[:nw], ref["winfo_len"])
+    np.testing.assert_array_equal(_np(ic.winfo_q_indices)[:nw], ref["winfo_q"])
+    if n:
+        np.testing.assert_array_equal(_np(dcs)[:n], ref["dense_cache_seqlens"])
+        np.testing.assert_array_equal(_np(scs)[:n], ref["sparse_cache_seqlens"])
+        for got, exp, wm in ((dpt, ref["dense_page_table"], ref["dense_pt_written"]),
+                             (spt, ref["sparse_page_table"], ref["sparse_pt_written"])):
+            g = _np(got)[:n]
+            np.testing.assert_array_equal(g[wm], exp[wm])
+            assert (g[~wm] == -5).all()
+    assert (_np(ic.kv_last_page_len) == -9).all()

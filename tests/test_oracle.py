@@ -348,3 +348,40 @@ def test_planted_planner_mistake_is_caught(monkeypatch):
     with pytest.raises(AssertionError):
         test_plan_int16_wraparound()
     monkeypatch.setattr(O, "_int16", real)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_plan_fa3_matches_bruteforce(seed):
+    """FA3 planner extras, restated per segment from the brute-force planner:
+    padded dense / sparse page tables (the FA3 indices kernel's writes,
+    utils_sglang.cu:1041-1078) and cache lengths (utils_sglang.cu:966-977)."""
+    batch = W.random_small(seed)
+    P, H = batch.page_size, batch.num_kv_heads
+    L = batch.seq_lens.numpy()
+    args = (L, batch.req_to_token.numpy(), batch.req_indices.numpy(), P, H, batch.topk, batch.bos, batch.eos,
+            batch.max_chunk)
+    stride = max(1, batch.max_pages_per_request - 3)  # also exercises rows longer than the table
+    got = O.plan_decode_fa3(*args, stride)
+    dptr, dense, sptr, sparse, last, wq, wo, wl = brute_plan(*args)
+    budget = batch.topk + batch.bos + batch.eos
+    for b in range(len(L)):
+        nb = _py_trunc_div(int(L[b]) + P - 1, P)
+        for h in range(H):
+            s = b * H + h
+            assert got["dense_cache_seqlens"][s] == L[b]
+            assert got["sparse_cache_seqlens"][s] == min((budget - 1) * P + last[s], int(L[b]))
+            for j in range(stride):
+                if j < nb:
+                    assert got["dense_pt_written"][s, j] and got["dense_page_table"][s, j] == dense[dptr[s] + j]
+                else:
+                    assert not got["dense_pt_written"][s, j]
+            if nb <= budget:
+                slots = list(range(nb))
+            else:
+                slots = list(range(batch.bos)) + [budget - 1 - e for e in range(batch.eos)]
+            for i in range(stride):
+                if i in slots:
+                    assert got["sparse_pt_written"][s, i] and got["sparse_page_table"][s, i] == sparse[sptr[s] + i]
+                else:
+                    assert not got["sparse_pt_written"][s, i]
+    np.testing.assert_array_equal(got["dense_indices"], np.asarray(dense, dtype=np.int32))

@@ -26,6 +26,7 @@
 // kernel's for the same query.
 #include "vtx_device.h"
 #include "vtx_host.h"
+#include "vtx_score.h"
 #include "vtx_select.h"
 
 namespace {
@@ -120,80 +121,12 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
   }
 }
 
-// One wave pass over `cnt` <= kPass consecutive pages of a segment; lane l
-// (< cnt) holds the l-th page's centroid row id in my_row.  A row is split over
-// LPR lanes x VPL 16-byte vectors (kRowsPerLoad = 64 / LPR rows per wave-wide
-// load, kSlots = kPass / kRowsPerLoad rows per lane), every lane issues its
-// row loads before any arithmetic, and a reduce-scatter over the LPR lanes
-// leaves each finished score on one lane.  Returns that score (fp32) and its
-// position in the pass in *r; *r = -1 on lanes that own no page.
-template <int LPR, int VPL, int kPass>
-__device__ __forceinline__ float score_pass(const FusedArgs& a, int my_row, int cnt,
-                                            const float (&xs)[VPL][8], int grp, int col, int* r) {
-  constexpr int kRowsPerLoad = vtx::kWave / LPR;
-  constexpr int kSlots = kPass / kRowsPerLoad;
-  constexpr int kBatch = VPL <= 2 ? kSlots : (kSlots < 2 ? kSlots : 2);  // slots loaded together
-  static_assert(kSlots >= 1 && kSlots <= LPR && kSlots * kRowsPerLoad == kPass, "pass geometry");
-  const int D = a.dim;
-  int first = __shfl(my_row, 0, vtx::kWave);
-  if (first < 0 || first >= a.y_rows) first = 0;
-  float acc[kSlots];
-#pragma unroll
-  for (int i0 = 0; i0 < kSlots; i0 += kBatch) {
-    vtx::U4 buf[kBatch][VPL];
-    bool live[kBatch];
-#pragma unroll
-    for (int ii = 0; ii < kBatch; ++ii) {
-      const int row = __shfl(my_row, (i0 + ii) * kRowsPerLoad + grp, vtx::kWave);
-      live[ii] = row >= 0 && row < a.y_rows;
-      if ((i0 + ii) * kRowsPerLoad < cnt) {  // wave-uniform: slots past the pass are skipped
-        const uint16_t* yr = a.y + (long long)(live[ii] ? row : first) * D;
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::ld16_stream(yr + (v * LPR + col) * 8);
-      } else {
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[ii][v] = vtx::U4{0u, 0u, 0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int ii = 0; ii < kBatch; ++ii) {
-      const float s = vtx::dot_row<VPL>(buf[ii], xs);
-      acc[i0 + ii] = live[ii] ? s : 0.f;
-    }
-  }
-  // Reduce-scatter over the slots (lane keeps slot bits of col from the top),
-  // then fold the lanes that still share a slot.  The strides run LPR/2 down
-  // to 1 in both parts: the same summation tree as gemv.hip.
-#pragma unroll
-  for (int half = kSlots / 2, stride = LPR / 2; half >= 1; half >>= 1, stride >>= 1) {
-    const bool upper = (col & stride) != 0;
-#pragma unroll
-    for (int t = 0; t < half; ++t) {
-      const float send = upper ? acc[t] : acc[t + half];
-      const float keep = upper ? acc[t + half] : acc[t];
-      acc[t] = keep + __shfl_xor(send, stride, vtx::kWave);
-    }
-  }
-  constexpr int kShare = LPR / kSlots;  // lanes holding the same slot
-#pragma unroll
-  for (int d = kShare / 2; d >= 1; d >>= 1) acc[0] += __shfl_xor(acc[0], d, vtx::kWave);
-  const int pos = (col / kShare) * kRowsPerLoad + grp;
-  *r = ((col % kShare) == 0 && pos < cnt) ? pos : -1;
-  return acc[0];
-}
-
-// Pages per wave pass: 64 when a row is one 16-byte vector per lane, else 32.
-template <int VPL>
-constexpr int segment_pass() {
-  return VPL == 1 ? 64 : 32;
-}
-
 // One workgroup per segment: scores into LDS, select in LDS.
 template <int T, int LPR, int VPL>
 __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
-  constexpr int kPass = segment_pass<VPL>();
+  constexpr int kPass = vtx::segment_pass<VPL>();
   constexpr int kQRegs = VPL <= 2 ? 2 : 1;  // query rows prefetched
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
@@ -264,7 +197,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       have_mean = true;
     }
     int r;
-    const float sc = score_pass<LPR, VPL, kPass>(a, my_row, cnt, xs, grp, col, &r);
+    const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
     if (r >= 0) {
       const uint32_t sb = vtx::f32_to_bf16(sc);
@@ -384,7 +317,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
       have_mean = true;
     }
     int r;
-    const float sc = score_pass<LPR, VPL, kPass>(a, my_row, cnt, xs, grp, col, &r);
+    const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
     if (r >= 0) store_coherent(a.score + start + p0 + r, (uint16_t)vtx::f32_to_bf16(sc));
   }
   // (wave 0 of chunk 0 always has pages, so the mean has been stored)

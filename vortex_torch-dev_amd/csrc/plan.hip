@@ -37,6 +37,15 @@ struct PlanArgs {
   int64_t wcap;
   int32_t* wnum;
   int32_t* wchunk;
+  // FA3 variant outputs (all optional): per-segment page tables
+  // [pt_rows, pt_stride] and per-segment cache sequence lengths
+  int32_t* dpt;
+  int32_t* spt;
+  int64_t pt_rows;
+  int64_t pt_stride;
+  int32_t* dcs;
+  int32_t* scs;
+  int64_t cs_len;
   int32_t page, heads, topk, bos, eos, chunk;
 };
 
@@ -110,11 +119,18 @@ __global__ __launch_bounds__(kThreads) void plan_decode_kernel(PlanArgs a) {
 
   if (head_slab) {
     const int rem = L % a.page;
+    const int last_page = (rem == 0) ? a.page : rem;
     for (int h = tid; h < H; h += kThreads) {
       const long long s = (long long)b * H + h;
       a.dense_indptr[s] = (int32_t)(dbase + (long long)h * n);
       a.sparse_indptr[s] = (int32_t)(sbase + (long long)h * sn);
-      a.last_len[s] = (rem == 0) ? a.page : rem;
+      if (a.last_len) a.last_len[s] = last_page;
+      if (s < a.cs_len) {
+        // FA3: the KV length each segment's attention reads (all of it, or
+        // the budget's pages with the last one partial)
+        if (a.dcs) a.dcs[s] = L;
+        if (a.scs) a.scs[s] = (int32_t)min((long long)(budget - 1) * a.page + last_page, (long long)L);
+      }
     }
     const int mid = middle_pages(n, a);
     const int ck = (mid + a.chunk - 1) / a.chunk;
@@ -153,56 +169,49 @@ __global__ __launch_bounds__(kThreads) void plan_decode_kernel(PlanArgs a) {
   const bool copy_all = (n <= budget);
   const bool is_bos = j < a.bos;
   const bool is_eos = j >= (long long)n - a.eos;
+  // position of this page in the segment's sparse list (-1: left for top-k)
+  const long long lp = (copy_all || is_bos) ? j : (is_eos ? budget - n + j : -1);
   for (int h = 0; h < H; ++h) {
     const int32_t v = phys * H + h;
+    const long long s = (long long)b * H + h;
     const long long di = dbase + (long long)h * n + j;
     if (di < a.dense_cap) a.dense_idx[di] = v;
-    long long si = -1;
-    if (copy_all) {
-      si = sbase + (long long)h * sn + j;
-    } else if (is_bos) {
-      si = sbase + (long long)h * budget + j;
-    } else if (is_eos) {
-      si = sbase + (long long)h * budget + (budget - n + j);
-    }
+    const long long si = lp >= 0 ? sbase + (long long)h * sn + lp : -1;
     if (si >= 0 && si < a.sparse_cap) a.sparse_idx[si] = v;
+    if (s < a.pt_rows) {
+      if (a.dpt && j < a.pt_stride) a.dpt[s * a.pt_stride + j] = v;
+      if (a.spt && lp >= 0 && lp < a.pt_stride) a.spt[s * a.pt_stride + lp] = v;
+    }
   }
 }
 
-}  // namespace
-
-extern "C" int vtx_plan_decode(
-    const int32_t* cached_seq_lens, int32_t batch_size, int32_t* dense_kv_indptr,
-    int32_t* dense_kv_indices, int64_t dense_kv_indices_len, int32_t* sparse_kv_indptr,
-    int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len, int32_t* kv_last_page_len,
-    const int32_t* req_to_token, int64_t req_to_token_rows, int64_t req_to_token_stride,
-    const int64_t* req_indices, int32_t* winfo_q_indices, int32_t* winfo_kv_offsets,
-    int32_t* winfo_kv_lens, int64_t winfo_capacity, int32_t* winfo_num_workloads,
-    int32_t* winfo_chunk_size, int32_t page_size, int32_t num_kv_heads, int32_t topk_val,
-    int32_t page_reserved_bos, int32_t page_reserved_eos, int32_t max_chunk_size,
-    int32_t min_chunk_size, void* stream) {
-  vtx::clear_error();
-  (void)min_chunk_size;  // sizes the caller's winfo capacity only
-  if (batch_size < 0) return vtx::fail(VTX_E_INVALID, "plan_decode: batch_size < 0");
+// Validates the arguments shared by both planners, fills `a` and launches.
+// With kv_last_page_len NULL (the FA3 variant) that output is not written.
+int plan_launch(PlanArgs& a, const char* what, const int32_t* cached_seq_lens, int32_t batch_size,
+                int32_t* dense_kv_indptr, int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                int32_t* sparse_kv_indptr, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                int32_t* kv_last_page_len, bool need_last_len, const int32_t* req_to_token,
+                int64_t req_to_token_rows, int64_t req_to_token_stride, const int64_t* req_indices,
+                int32_t* winfo_q_indices, int32_t* winfo_kv_offsets, int32_t* winfo_kv_lens, int64_t winfo_capacity,
+                int32_t* winfo_num_workloads, int32_t* winfo_chunk_size, int32_t page_size, int32_t num_kv_heads,
+                int32_t topk_val, int32_t page_reserved_bos, int32_t page_reserved_eos, int32_t max_chunk_size,
+                void* stream) {
+  if (batch_size < 0) return vtx::fail(VTX_E_INVALID, "%s: batch_size < 0", what);
   if (page_size < 1 || num_kv_heads < 1 || max_chunk_size < 1)
     return vtx::fail(VTX_E_INVALID,
-                     "plan_decode: page_size (%d), num_kv_heads (%d) and max_chunk_size (%d) "
-                     "must be >= 1",
+                     "%s: page_size (%d), num_kv_heads (%d) and max_chunk_size (%d) must be >= 1", what,
                      page_size, num_kv_heads, max_chunk_size);
   if (topk_val < 0 || page_reserved_bos < 0 || page_reserved_eos < 0)
-    return vtx::fail(VTX_E_INVALID, "plan_decode: topk/bos/eos must be >= 0");
-  if (!cached_seq_lens && batch_size > 0)
-    return vtx::fail(VTX_E_INVALID, "plan_decode: null cached_seq_lens");
+    return vtx::fail(VTX_E_INVALID, "%s: topk/bos/eos must be >= 0", what);
+  if (!cached_seq_lens && batch_size > 0) return vtx::fail(VTX_E_INVALID, "%s: null cached_seq_lens", what);
   if (!dense_kv_indptr || !sparse_kv_indptr || !winfo_num_workloads || !winfo_chunk_size)
-    return vtx::fail(VTX_E_INVALID, "plan_decode: null output pointer");
-  if (batch_size > 0 && (!dense_kv_indices || !sparse_kv_indices || !kv_last_page_len ||
+    return vtx::fail(VTX_E_INVALID, "%s: null output pointer", what);
+  if (batch_size > 0 && (!dense_kv_indices || !sparse_kv_indices || (need_last_len && !kv_last_page_len) ||
                          !req_to_token || !req_indices || req_to_token_stride < 1))
-    return vtx::fail(VTX_E_INVALID, "plan_decode: null input/output pointer or empty req_to_token");
-  if (batch_size > 0 && (winfo_capacity > 0) &&
-      (!winfo_q_indices || !winfo_kv_offsets || !winfo_kv_lens))
-    return vtx::fail(VTX_E_INVALID, "plan_decode: null winfo pointer");
+    return vtx::fail(VTX_E_INVALID, "%s: null input/output pointer or empty req_to_token", what);
+  if (batch_size > 0 && (winfo_capacity > 0) && (!winfo_q_indices || !winfo_kv_offsets || !winfo_kv_lens))
+    return vtx::fail(VTX_E_INVALID, "%s: null winfo pointer", what);
 
-  PlanArgs a;
   a.seq_lens = cached_seq_lens;
   a.batch = batch_size;
   a.dense_indptr = dense_kv_indptr;
@@ -235,5 +244,61 @@ extern "C" int vtx_plan_decode(
   if (slabs > 65535) return vtx::fail(VTX_E_INVALID, "plan_decode: req_to_token row too long");
   dim3 grid(batch_size > 0 ? batch_size : 1, (unsigned)slabs);
   plan_decode_kernel<<<grid, kThreads, 0, vtx::as_stream(stream)>>>(a);
-  return vtx::check_launch("plan_decode");
+  return vtx::check_launch(what);
+}
+
+}  // namespace
+
+extern "C" int vtx_plan_decode(
+    const int32_t* cached_seq_lens, int32_t batch_size, int32_t* dense_kv_indptr,
+    int32_t* dense_kv_indices, int64_t dense_kv_indices_len, int32_t* sparse_kv_indptr,
+    int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len, int32_t* kv_last_page_len,
+    const int32_t* req_to_token, int64_t req_to_token_rows, int64_t req_to_token_stride,
+    const int64_t* req_indices, int32_t* winfo_q_indices, int32_t* winfo_kv_offsets,
+    int32_t* winfo_kv_lens, int64_t winfo_capacity, int32_t* winfo_num_workloads,
+    int32_t* winfo_chunk_size, int32_t page_size, int32_t num_kv_heads, int32_t topk_val,
+    int32_t page_reserved_bos, int32_t page_reserved_eos, int32_t max_chunk_size,
+    int32_t min_chunk_size, void* stream) {
+  vtx::clear_error();
+  (void)min_chunk_size;  // sizes the caller's winfo capacity only
+  PlanArgs a{};
+  return plan_launch(a, "plan_decode", cached_seq_lens, batch_size, dense_kv_indptr, dense_kv_indices,
+                     dense_kv_indices_len, sparse_kv_indptr, sparse_kv_indices, sparse_kv_indices_len,
+                     kv_last_page_len, true, req_to_token, req_to_token_rows, req_to_token_stride, req_indices,
+                     winfo_q_indices, winfo_kv_offsets, winfo_kv_lens, winfo_capacity, winfo_num_workloads,
+                     winfo_chunk_size, page_size, num_kv_heads, topk_val, page_reserved_bos, page_reserved_eos,
+                     max_chunk_size, stream);
+}
+
+extern "C" int vtx_plan_decode_fa3(
+    const int32_t* cached_seq_lens, int32_t batch_size, int32_t* dense_kv_indptr,
+    int32_t* dense_kv_indices, int64_t dense_kv_indices_len, int32_t* sparse_kv_indptr,
+    int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len, int32_t* dense_page_table,
+    int32_t* dense_cache_seqlens, int32_t* sparse_page_table, int32_t* sparse_cache_seqlens,
+    int64_t page_table_rows, int64_t page_table_stride, int64_t cache_seqlens_len,
+    const int32_t* req_to_token, int64_t req_to_token_rows, int64_t req_to_token_stride,
+    const int64_t* req_indices, int32_t* winfo_q_indices, int32_t* winfo_kv_offsets,
+    int32_t* winfo_kv_lens, int64_t winfo_capacity, int32_t* winfo_num_workloads,
+    int32_t* winfo_chunk_size, int32_t page_size, int32_t num_kv_heads, int32_t topk_val,
+    int32_t page_reserved_bos, int32_t page_reserved_eos, int32_t max_chunk_size,
+    int32_t min_chunk_size, void* stream) {
+  vtx::clear_error();
+  (void)min_chunk_size;
+  if (batch_size > 0 && (!dense_page_table || !sparse_page_table || !dense_cache_seqlens || !sparse_cache_seqlens))
+    return vtx::fail(VTX_E_INVALID, "plan_decode_fa3: null page table or cache_seqlens");
+  if (page_table_rows < 0 || page_table_stride < 0 || cache_seqlens_len < 0)
+    return vtx::fail(VTX_E_INVALID, "plan_decode_fa3: negative page table or cache_seqlens size");
+  PlanArgs a{};
+  a.dpt = dense_page_table;
+  a.spt = sparse_page_table;
+  a.pt_rows = page_table_rows;
+  a.pt_stride = page_table_stride;
+  a.dcs = dense_cache_seqlens;
+  a.scs = sparse_cache_seqlens;
+  a.cs_len = cache_seqlens_len;
+  return plan_launch(a, "plan_decode_fa3", cached_seq_lens, batch_size, dense_kv_indptr, dense_kv_indices,
+                     dense_kv_indices_len, sparse_kv_indptr, sparse_kv_indices, sparse_kv_indices_len, nullptr,
+                     false, req_to_token, req_to_token_rows, req_to_token_stride, req_indices, winfo_q_indices,
+                     winfo_kv_offsets, winfo_kv_lens, winfo_capacity, winfo_num_workloads, winfo_chunk_size,
+                     page_size, num_kv_heads, topk_val, page_reserved_bos, page_reserved_eos, max_chunk_size, stream);
 }

@@ -19,6 +19,7 @@
 // on the VALU and are bound by HBM and latency.
 #include "vtx_device.h"
 #include "vtx_host.h"
+#include "vtx_score.h"
 
 #include <cstring>
 
@@ -148,6 +149,61 @@ __global__ __launch_bounds__(kThreads) void gemm_ragged_kernel(GemmArgs a) {
   }
 }
 
+// Fast path for one y row per position (C == 1) and BATCHED x, the GeMM of
+// the GQA flow: a wave takes up to kPass positions of a workload at once,
+// issues every y row load before any arithmetic and scores kG query rows of
+// the segment per load (vtx::score_pass_multi); K = LPR * VPL * 8.
+template <int LPR, int VPL, int kG>
+__global__ __launch_bounds__(kThreads) void gemm_rows_kernel(GemmArgs a) {
+  constexpr int kPass = vtx::segment_pass<VPL>();
+  const int lane = vtx::lane_id();
+  const int grp = lane / LPR;
+  const int col = lane % LPR;
+  const int wid = blockIdx.x * kWavesPerBlock + threadIdx.x / vtx::kWave;
+  const int waves = gridDim.x * kWavesPerBlock;
+  const int G = a.x.d0, K = a.x.d1;
+  const int nw = workload_count(a.w);
+  for (int i = wid; i < nw; i += waves) {
+    int q, len;
+    long long off;
+    if (!workload(a.w, i, &q, &off, &len)) continue;
+    const long long rx = opnd_row(a.x, a.w, q, off);
+    if (rx < 0) continue;
+    for (int p0 = 0; p0 < len; p0 += kPass) {
+      const int cnt = min(kPass, len - p0);
+      int my_row = -1;
+      if (lane < cnt) {
+        const long long r = opnd_row(a.y, a.w, q, off + p0 + lane);
+        my_row = r >= 0 ? (int)r : -1;
+      }
+      for (int g0 = 0; g0 < G; g0 += kG) {
+        float xs[kG][VPL][8];
+#pragma unroll
+        for (int gg = 0; gg < kG; ++gg)
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) {
+            if (g0 + gg < G) {
+              vtx::unpack8(vtx::ld16(a.x.p + (rx * G + g0 + gg) * (long long)K + (v * LPR + col) * 8), xs[gg][v]);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) xs[gg][v][e] = 0.f;
+            }
+          }
+        int r;
+        float sc[kG];
+        vtx::score_pass_multi<LPR, VPL, kPass, kG>(a.y.p, a.y.rows, K, my_row, cnt, xs, grp, col, &r, sc);
+        const int rrow = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row of the lane's position
+        if (r >= 0 && rrow >= 0) {
+          const long long p = off + p0 + r;
+#pragma unroll
+          for (int gg = 0; gg < kG; ++gg)
+            if (g0 + gg < G) a.o[p * G + g0 + gg] = (uint16_t)vtx::f32_to_bf16(sc[gg]);
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------- elementwise binary / unary
 // Binary: o[p, i, j] = op(x[rx, i', j'], y[ry, i'', j'']) where an operand
 // axis of size 1 broadcasts.  bf16 in and out; max / min compare the values,
@@ -188,54 +244,70 @@ __device__ __forceinline__ float unary_op(int op, float xv, float alpha, float b
   }
 }
 
-// kVec: 8 consecutive j per lane (o_d1 % 8 == 0 and no operand broadcasts
-// along j); otherwise one element per lane.
+// One workgroup per workload; kVec: 8 consecutive j per lane (o_d1 % 8 == 0
+// and no operand broadcasts along j), otherwise one element per lane.  Each
+// thread takes kU items per round and issues all their loads before any
+// arithmetic.
 template <bool kBinary, bool kVec>
 __global__ __launch_bounds__(kThreads) void elementwise_ragged_kernel(EwArgs a) {
   constexpr int kW = kVec ? 8 : 1;
-  const int lane = vtx::lane_id();
-  const int wid = blockIdx.x * kWavesPerBlock + threadIdx.x / vtx::kWave;
-  const int waves = gridDim.x * kWavesPerBlock;
+  constexpr int kU = 4;
+  const int tid = threadIdx.x;
   const int nj = a.o_d1 / kW;
   const int per_pos = a.o_d0 * nj;
   const int nw = workload_count(a.w);
-  for (int i = wid; i < nw; i += waves) {
+  for (int i = blockIdx.x; i < nw; i += gridDim.x) {
     int q, len;
     long long off;
     if (!workload(a.w, i, &q, &off, &len)) continue;
     const long long items = (long long)len * per_pos;
-    for (long long it = lane; it < items; it += vtx::kWave) {
-      const int t = (int)(it / per_pos);
-      const int e = (int)(it - (long long)t * per_pos);
-      const int i0 = e / nj;
-      const int j0 = (e - i0 * nj) * kW;
-      const long long p = off + t;
-      const long long rx = opnd_row(a.x, a.w, q, p);
-      const long long ry = kBinary ? opnd_row(a.y, a.w, q, p) : 0;
-      if (rx < 0 || ry < 0) continue;
-      const long long xo = (rx * a.x.d0 + (a.x.d0 == 1 ? 0 : i0)) * a.x.d1;
-      const long long yo = kBinary ? (ry * a.y.d0 + (a.y.d0 == 1 ? 0 : i0)) * a.y.d1 : 0;
-      uint16_t* op = a.o + (p * a.o_d0 + i0) * a.o_d1 + j0;
-      if (kVec) {
-        float xf[8], yf[8];
-        vtx::unpack8(vtx::ld16(a.x.p + xo + j0), xf);
-        if (kBinary) vtx::unpack8(vtx::ld16(a.y.p + yo + j0), yf);
-        uint32_t r[8];
+    for (long long base = 0; base < items; base += (long long)kThreads * kU) {
+      vtx::U4 xv[kU], yv[kU];
+      long long oi[kU];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-          r[k] = vtx::f32_to_bf16(kBinary ? binary_op(a.op, xf[k], yf[k], a.alpha, a.beta)
-                                          : unary_op(a.op, xf[k], a.alpha, a.beta));
-        vtx::st16(op, vtx::U4{r[0] | (r[1] << 16), r[2] | (r[3] << 16), r[4] | (r[5] << 16), r[6] | (r[7] << 16)});
-      } else {
-        const float xv = vtx::bf16_to_f32(a.x.p[xo + (a.x.d1 == 1 ? 0 : j0)]);
-        float r;
-        if (kBinary) {
-          const float yv = vtx::bf16_to_f32(a.y.p[yo + (a.y.d1 == 1 ? 0 : j0)]);
-          r = binary_op(a.op, xv, yv, a.alpha, a.beta);
+      for (int u = 0; u < kU; ++u) {
+        const long long it = base + (long long)u * kThreads + tid;
+        oi[u] = -1;
+        if (it >= items) continue;
+        const int t = (int)(it / per_pos);
+        const int e = (int)(it - (long long)t * per_pos);
+        const int i0 = e / nj;
+        const int j0 = (e - i0 * nj) * kW;
+        const long long p = off + t;
+        const long long rx = opnd_row(a.x, a.w, q, p);
+        const long long ry = kBinary ? opnd_row(a.y, a.w, q, p) : 0;
+        if (rx < 0 || ry < 0) continue;
+        const long long xo = (rx * a.x.d0 + (a.x.d0 == 1 ? 0 : i0)) * a.x.d1;
+        const long long yo = kBinary ? (ry * a.y.d0 + (a.y.d0 == 1 ? 0 : i0)) * a.y.d1 : 0;
+        oi[u] = (p * a.o_d0 + i0) * a.o_d1 + j0;
+        if (kVec) {
+          xv[u] = vtx::ld16(a.x.p + xo + j0);
+          if (kBinary) yv[u] = vtx::ld16(a.y.p + yo + j0);
         } else {
-          r = unary_op(a.op, xv, a.alpha, a.beta);
+          xv[u].x = a.x.p[xo + (a.x.d1 == 1 ? 0 : j0)];
+          if (kBinary) yv[u].x = a.y.p[yo + (a.y.d1 == 1 ? 0 : j0)];
         }
-        *op = (uint16_t)vtx::f32_to_bf16(r);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        if (oi[u] < 0) continue;
+        if (kVec) {
+          float xf[8], yf[8];
+          vtx::unpack8(xv[u], xf);
+          if (kBinary) vtx::unpack8(yv[u], yf);
+          uint32_t r[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            r[k] = vtx::f32_to_bf16(kBinary ? binary_op(a.op, xf[k], yf[k], a.alpha, a.beta)
+                                            : unary_op(a.op, xf[k], a.alpha, a.beta));
+          vtx::st16(a.o + oi[u],
+                    vtx::U4{r[0] | (r[1] << 16), r[2] | (r[3] << 16), r[4] | (r[5] << 16), r[6] | (r[7] << 16)});
+        } else {
+          const float xf = vtx::bf16_to_f32(xv[u].x);
+          const float res = kBinary ? binary_op(a.op, xf, vtx::bf16_to_f32(yv[u].x), a.alpha, a.beta)
+                                    : unary_op(a.op, xf, a.alpha, a.beta);
+          a.o[oi[u]] = (uint16_t)vtx::f32_to_bf16(res);
+        }
       }
     }
   }
@@ -273,44 +345,85 @@ __device__ __forceinline__ float racc_out(const RAcc& r, int type, int count) {
   }
 }
 
+__device__ __forceinline__ float racc_merge(float a, float b, int type) {
+  if (type == VTX_REDUCE_MAX) return fmaxf(a, b);
+  if (type == VTX_REDUCE_MIN) return fminf(a, b);
+  return a + b;
+}
+
+// One workgroup per workload.  Along a contiguous axis that is a multiple of
+// 8 wide, L lanes (a power of two <= 16 dividing the axis' 16-byte vectors)
+// share an output: each reads every L-th vector, kU loads issued together,
+// and the L partials are merged by an xor tree.  Otherwise a lane computes
+// one output, reading kU elements per round.
 __global__ __launch_bounds__(kThreads) void reduce_ragged_kernel(ReduceArgs a) {
-  const int lane = vtx::lane_id();
-  const int wid = blockIdx.x * kWavesPerBlock + threadIdx.x / vtx::kWave;
-  const int waves = gridDim.x * kWavesPerBlock;
+  constexpr int kU = 4;
+  const int tid = threadIdx.x;
   const int D0 = a.x.d0, D1 = a.x.d1;
   const int per_pos = a.dim == 1 ? D1 : D0;
   const int count = a.dim == 1 ? D0 : D1;
   const bool vec = a.dim == 2 && (D1 % 8) == 0;
+  const int nvec = D1 / 8;
+  int L = 1;
+  if (vec)
+    while (L < 16 && nvec % (2 * L) == 0) L *= 2;
   const float init = a.type == VTX_REDUCE_MAX ? -INFINITY : (a.type == VTX_REDUCE_MIN ? INFINITY : 0.f);
   const int nw = workload_count(a.w);
-  for (int i = wid; i < nw; i += waves) {
+  for (int i = blockIdx.x; i < nw; i += gridDim.x) {
     int q, len;
     long long off;
     if (!workload(a.w, i, &q, &off, &len)) continue;
-    const long long items = (long long)len * per_pos;
-    for (long long it = lane; it < items; it += vtx::kWave) {
-      const int t = (int)(it / per_pos);
-      const int e = (int)(it - (long long)t * per_pos);
+    const long long outputs = (long long)len * per_pos;
+    const long long tasks = outputs * L;  // L lanes per output (aligned groups within a wave)
+    for (long long base = 0; base < tasks; base += kThreads) {
+      const long long it = base + tid;
+      const long long oidx = it / L;
+      const int sub = (int)(it - oidx * L);
+      const bool in = it < tasks;
+      long long t = in ? oidx / per_pos : 0;
+      const int e = in ? (int)(oidx - t * per_pos) : 0;
       const long long p = off + t;
-      const long long rx = opnd_row(a.x, a.w, q, p);
-      if (rx < 0) continue;
-      const uint16_t* tile = a.x.p + rx * (long long)D0 * D1;
+      const long long rx = in ? opnd_row(a.x, a.w, q, p) : -1;
       RAcc r{0.f, init, 0.f};
-      if (a.dim == 1) {
-        for (int d = 0; d < D0; ++d) racc_add(r, vtx::bf16_to_f32(tile[(long long)d * D1 + e]), a.type);
-      } else if (vec) {
-        const uint16_t* row = tile + (long long)e * D1;
-        for (int d = 0; d < D1; d += 8) {
-          float f[8];
-          vtx::unpack8(vtx::ld16(row + d), f);
+      if (rx >= 0) {
+        const uint16_t* tile = a.x.p + rx * (long long)D0 * D1;
+        if (vec) {
+          const uint16_t* row = tile + (long long)e * D1;
+          for (int v0 = sub; v0 < nvec; v0 += L * kU) {
+            vtx::U4 buf[kU];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) racc_add(r, f[k], a.type);
+            for (int u = 0; u < kU; ++u) {
+              const int v = v0 + u * L;
+              buf[u] = v < nvec ? vtx::ld16(row + v * 8) : vtx::U4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+              if (v0 + u * L >= nvec) break;
+              float f[8];
+              vtx::unpack8(buf[u], f);
+#pragma unroll
+              for (int k = 0; k < 8; ++k) racc_add(r, f[k], a.type);
+            }
+          }
+        } else {
+          const long long stride = a.dim == 1 ? D1 : 1;
+          const uint16_t* base_p = a.dim == 1 ? tile + e : tile + (long long)e * D1;
+          for (int d0 = 0; d0 < count; d0 += kU) {
+            float v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) v[u] = d0 + u < count ? vtx::bf16_to_f32(base_p[(d0 + u) * stride]) : 0.f;
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+              if (d0 + u < count) racc_add(r, v[u], a.type);
+          }
         }
-      } else {
-        const uint16_t* row = tile + (long long)e * D1;
-        for (int d = 0; d < D1; ++d) racc_add(r, vtx::bf16_to_f32(row[d]), a.type);
       }
-      a.o[p * per_pos + e] = (uint16_t)vtx::f32_to_bf16(racc_out(r, a.type, count));
+      float val = (a.type == VTX_REDUCE_MAX || a.type == VTX_REDUCE_MIN) ? r.m : r.s;
+      for (int d = L / 2; d >= 1; d >>= 1) val = racc_merge(val, __shfl_xor(val, d, vtx::kWave), a.type);
+      if (rx >= 0 && sub == 0) {
+        RAcc fin{val, val, 0.f};
+        a.o[p * per_pos + e] = (uint16_t)vtx::f32_to_bf16(racc_out(fin, a.type, count));
+      }
     }
   }
 }
@@ -358,42 +471,78 @@ __global__ __launch_bounds__(kThreads) void segment_scan_kernel(SegArgs a) {
     const int c = tid % cols;
     const int r0 = tid / cols;
     const bool active = r0 < per_col;
+    // Segments of up to kR pages per thread keep their values in registers
+    // (all loads issued at once, no second read).
+    constexpr int kR = 8;
+    const bool in_regs = cnt <= (long long)per_col * kR;  // uniform
+    float vals[kR];
+    if (in_regs) {
+#pragma unroll
+      for (int k = 0; k < kR; ++k) {
+        const long long r = r0 + (long long)k * per_col;
+        vals[k] = (active && r < cnt) ? vtx::bf16_to_f32(x[r * cols + c]) : 0.f;
+      }
+    }
     float m = kLow, s = 0.f;
-    if (active) {
-      for (long long r = r0; r < cnt; r += per_col) {
-        const float v = vtx::bf16_to_f32(x[r * cols + c]);
-        if (softmax) {
-          const float u = v * a.scale;
-          if (u > m) {
-            s = s * __expf(m - u) + 1.f;
-            m = u;
-          } else {
-            s += __expf(u - m);
-          }
+    auto add = [&](float v) {
+      if (softmax) {
+        const float u = v * a.scale;
+        if (u > m) {
+          s = s * __expf(m - u) + 1.f;
+          m = u;
         } else {
-          s = fmaf(v, v, s);
+          s += __expf(u - m);
         }
+      } else {
+        s = fmaf(v, v, s);
+      }
+    };
+    if (active) {
+      if (in_regs) {
+#pragma unroll
+        for (int k = 0; k < kR; ++k)
+          if (r0 + (long long)k * per_col < cnt) add(vals[k]);
+      } else {
+        for (long long r = r0; r < cnt; r += per_col) add(vtx::bf16_to_f32(x[r * cols + c]));
       }
     }
     pm[tid] = m;
     ps[tid] = s;
     __syncthreads();
-    if (tid < cols) {
-      float M = kLow;
-      for (int k = 0; k < per_col; ++k) M = fmaxf(M, pm[k * cols + tid]);
-      float S = 0.f;
-      for (int k = 0; k < per_col; ++k) S += softmax ? ps[k * cols + tid] * __expf(pm[k * cols + tid] - M) : ps[k * cols + tid];
-      pm[tid] = M;
-      ps[tid] = S;
+    // Tree merge of a column's per_col partials (thread r0 of the column
+    // absorbs r0 + h at step h): log2(per_col) steps.
+    for (int h = 1; h < per_col; h <<= 1) {
+      if (active && (r0 % (2 * h)) == 0 && r0 + h < per_col) {
+        const int o = (r0 + h) * cols + c;
+        if (softmax) {
+          const float m1 = pm[tid], m2 = pm[o];
+          const float M = fmaxf(m1, m2);
+          ps[tid] = ps[tid] * __expf(m1 - M) + ps[o] * __expf(m2 - M);
+          pm[tid] = M;
+        } else {
+          ps[tid] += ps[o];
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
     if (!active) return;
     const float M = pm[c], S = ps[c];
     const float norm = fmaxf(sqrtf(S), 1e-12f);
-    for (long long r = r0; r < cnt; r += per_col) {
-      const float v = vtx::bf16_to_f32(x[r * cols + c]);
-      const float o = softmax ? __expf(v * a.scale - M) / S : v / norm;
-      x[r * cols + c] = (uint16_t)vtx::f32_to_bf16(o);
+    if (in_regs) {
+#pragma unroll
+      for (int k = 0; k < kR; ++k) {
+        const long long r = r0 + (long long)k * per_col;
+        if (r < cnt) {
+          const float o = softmax ? __expf(vals[k] * a.scale - M) / S : vals[k] / norm;
+          x[r * cols + c] = (uint16_t)vtx::f32_to_bf16(o);
+        }
+      }
+    } else {
+      for (long long r = r0; r < cnt; r += per_col) {
+        const float v = vtx::bf16_to_f32(x[r * cols + c]);
+        const float o = softmax ? __expf(v * a.scale - M) / S : v / norm;
+        x[r * cols + c] = (uint16_t)vtx::f32_to_bf16(o);
+      }
     }
   } else {
     for (int c = tid; c < cols; c += kThreads) {
@@ -445,6 +594,15 @@ int grid_for(int64_t wcap) {
   const int cus = vtx::device_cu_count();
   long long g = (wcap + kWavesPerBlock - 1) / kWavesPerBlock;
   const long long cap = 8LL * (cus > 0 ? cus : 256);
+  if (g > cap) g = cap;
+  return (int)(g < 1 ? 1 : g);
+}
+
+// One workgroup per workload, at most 16 per CU (the rest loop).
+int grid_blocks(int64_t wcap) {
+  const int cus = vtx::device_cu_count();
+  long long g = wcap;
+  const long long cap = 16LL * (cus > 0 ? cus : 256);
   if (g > cap) g = cap;
   return (int)(g < 1 ? 1 : g);
 }
@@ -521,6 +679,23 @@ extern "C" int vtx_ragged_gemm(const uint16_t* x, int64_t x_rows, int32_t x_mode
   const int units = k / 8;
   const int grid = grid_for(winfo_capacity);
   hipStream_t s = vtx::as_stream(stream);
+  if (y_d0 == 1 && x_mode == VTX_ROWS_BATCHED) {
+    const bool two = x_d0 >= 2;
+    switch (k) {
+      case 64:
+        if (two) gemm_rows_kernel<8, 1, 2><<<grid, kThreads, 0, s>>>(a);
+        else gemm_rows_kernel<8, 1, 1><<<grid, kThreads, 0, s>>>(a);
+        return vtx::check_launch("ragged_gemm");
+      case 128:
+        if (two) gemm_rows_kernel<16, 1, 2><<<grid, kThreads, 0, s>>>(a);
+        else gemm_rows_kernel<16, 1, 1><<<grid, kThreads, 0, s>>>(a);
+        return vtx::check_launch("ragged_gemm");
+      case 256: gemm_rows_kernel<16, 2, 1><<<grid, kThreads, 0, s>>>(a); return vtx::check_launch("ragged_gemm");
+      case 512: gemm_rows_kernel<16, 4, 1><<<grid, kThreads, 0, s>>>(a); return vtx::check_launch("ragged_gemm");
+      case 576: gemm_rows_kernel<8, 9, 1><<<grid, kThreads, 0, s>>>(a); return vtx::check_launch("ragged_gemm");
+      default: break;
+    }
+  }
   if (units % 16 == 0) return launch_gemm<16>(a, grid, s);
   if (units % 8 == 0) return launch_gemm<8>(a, grid, s);
   if (units % 4 == 0) return launch_gemm<4>(a, grid, s);
@@ -567,7 +742,7 @@ int elementwise(bool binary, int32_t op, float alpha, float beta, const Opnd& xo
   a.beta = to_bf16_value(beta);
   const bool vec = (o_d1 % 8) == 0 && xo.d1 == o_d1 && (!binary || yo.d1 == o_d1) && vtx::aligned16(xo.p) &&
                    (!binary || vtx::aligned16(yo.p)) && vtx::aligned16(o);
-  const int grid = grid_for(wcap);
+  const int grid = grid_blocks(wcap);
   hipStream_t s = vtx::as_stream(stream);
   if (binary) {
     if (vec) elementwise_ragged_kernel<true, true><<<grid, kThreads, 0, s>>>(a);
@@ -631,7 +806,7 @@ extern "C" int vtx_ragged_reduce(const uint16_t* x, int64_t x_rows, int32_t d0, 
   a.o = o;
   a.dim = dim;
   a.type = reduce_type;
-  reduce_ragged_kernel<<<grid_for(winfo_capacity), kThreads, 0, vtx::as_stream(stream)>>>(a);
+  reduce_ragged_kernel<<<grid_blocks(winfo_capacity), kThreads, 0, vtx::as_stream(stream)>>>(a);
   return vtx::check_launch(what);
 }
 

@@ -34,6 +34,11 @@ _SIGNATURES = {
          _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
     ),
+    "vtx_plan_decode_fa3": (
+        [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp,
+         _vp, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
     "vtx_gemv_paged": (
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _i32, _vp],
         ctypes.c_int,
@@ -262,6 +267,72 @@ def plan_decode(
             int(page_size), H, int(topk_val), int(page_reserved_bos), int(page_reserved_eos),
             int(max_chunk_size), int(min_chunk_size), _stream(dev))
     _check(rc, "plan_decode")
+
+
+@_plain_args
+def plan_decode_fa3(
+    cached_seq_lens: torch.Tensor,
+    dense_kv_indptr: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    sparse_kv_indptr: torch.Tensor,
+    sparse_kv_indices: torch.Tensor,
+    dense_page_table: torch.Tensor,
+    dense_cache_seqlens: torch.Tensor,
+    sparse_page_table: torch.Tensor,
+    sparse_cache_seqlens: torch.Tensor,
+    req_to_token: torch.Tensor,
+    req_indices: torch.Tensor,
+    winfo_q_indices: torch.Tensor,
+    winfo_kv_offsets: torch.Tensor,
+    winfo_kv_lens: torch.Tensor,
+    winfo_num_workloads: torch.Tensor,
+    winfo_chunk_size: torch.Tensor,
+    page_size: int,
+    num_kv_heads: int,
+    topk_val: int,
+    page_reserved_bos: int,
+    page_reserved_eos: int,
+    max_chunk_size: int,
+    min_chunk_size: int,
+) -> None:
+    """FA3 decode planner: the block tables and workload list of plan_decode
+    plus per-segment padded page tables and cache sequence lengths."""
+    lib = load_library()
+    i32 = torch.int32
+    tensors = (cached_seq_lens, dense_kv_indptr, dense_kv_indices, sparse_kv_indptr, sparse_kv_indices,
+               dense_page_table, dense_cache_seqlens, sparse_page_table, sparse_cache_seqlens, req_to_token,
+               winfo_q_indices, winfo_kv_offsets, winfo_kv_lens, winfo_num_workloads, winfo_chunk_size)
+    dev = _require_gpu(req_indices, *tensors)
+    for t in tensors:
+        _req(t, i32, "FA3 planner int32 buffer")
+    _req(req_indices, torch.int64, "req_indices")
+    B = int(cached_seq_lens.shape[0])
+    H = int(num_kv_heads)
+    if req_to_token.dim() != 2:
+        raise RuntimeError("vortex_torch: req_to_token must be 2-D [rows, max_tokens]")
+    if dense_page_table.dim() != 2 or sparse_page_table.shape != dense_page_table.shape:
+        raise RuntimeError("vortex_torch: dense and sparse page tables must be 2-D and of one shape")
+    if req_indices.numel() < B:
+        raise RuntimeError("vortex_torch: req_indices shorter than cached_seq_lens")
+    if dense_kv_indptr.numel() < B * H + 1 or sparse_kv_indptr.numel() < B * H + 1:
+        raise RuntimeError(f"vortex_torch: indptr buffers need {B * H + 1} entries")
+    if winfo_num_workloads.numel() < 1 or winfo_chunk_size.numel() < 1:
+        raise RuntimeError("vortex_torch: winfo_num_workloads / winfo_chunk_size need 1 entry")
+    wcap = min(winfo_q_indices.numel(), winfo_kv_offsets.numel(), winfo_kv_lens.numel())
+    cs_len = min(dense_cache_seqlens.numel(), sparse_cache_seqlens.numel())
+    with _on_device(dev):
+        rc = lib.vtx_plan_decode_fa3(
+            cached_seq_lens.data_ptr(), B,
+            dense_kv_indptr.data_ptr(), dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            sparse_kv_indptr.data_ptr(), sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
+            dense_page_table.data_ptr(), dense_cache_seqlens.data_ptr(), sparse_page_table.data_ptr(),
+            sparse_cache_seqlens.data_ptr(), int(dense_page_table.shape[0]), int(dense_page_table.shape[1]), cs_len,
+            req_to_token.data_ptr(), int(req_to_token.shape[0]), int(req_to_token.shape[1]), req_indices.data_ptr(),
+            winfo_q_indices.data_ptr(), winfo_kv_offsets.data_ptr(), winfo_kv_lens.data_ptr(), wcap,
+            winfo_num_workloads.data_ptr(), winfo_chunk_size.data_ptr(),
+            int(page_size), H, int(topk_val), int(page_reserved_bos), int(page_reserved_eos),
+            int(max_chunk_size), int(min_chunk_size), _stream(dev))
+    _check(rc, "plan_decode_fa3")
 
 
 @_plain_args

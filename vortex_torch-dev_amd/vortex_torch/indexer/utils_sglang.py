@@ -2,9 +2,11 @@
 
 ``plan_decode`` is called once per decode step by the attention backend,
 before any layer runs: it fills the context's block tables and workload list
-(reference vortex_torch/indexer/utils_sglang.py:15-44).  The prefill, FA3 and
-transpose helpers of the reference serve other attention paths; they exist
-here under the same names and raise ``NotImplementedError``.
+(reference vortex_torch/indexer/utils_sglang.py:15-44); ``plan_decode_fa3``
+does the same for the FA3 attention backend and also fills its padded page
+tables (utils_sglang.py:135-168).  The prefill and transpose helpers of the
+reference serve other attention paths; they exist here under the same names
+and raise ``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -53,8 +55,45 @@ def plan_prefill_fa3(*args, **kwargs):
     return _C.sglang_plan_prefill_fa3(*args, **kwargs)
 
 
-def plan_decode_fa3(*args, **kwargs):
-    return _C.sglang_plan_decode_fa3(*args, **kwargs)
+def plan_decode_fa3(
+    cached_seq_lens: torch.Tensor,
+    req_to_token: torch.Tensor,
+    req_indices: torch.Tensor,
+    dense_page_table: torch.Tensor,
+    dense_cache_seqlens: torch.Tensor,
+    sparse_page_table: torch.Tensor,
+    sparse_cache_seqlens: torch.Tensor,
+    ctx: Context,
+) -> None:
+    """FA3 decode planner (reference utils_sglang.py:135-168): ctx's block
+    tables and workload list plus the caller's per-segment page tables and
+    cache sequence lengths."""
+    _C.sglang_plan_decode_fa3(
+        cached_seq_lens,
+        ctx.dense_kv_indptr,
+        ctx.dense_kv_indices,
+        ctx.sparse_kv_indptr,
+        ctx.sparse_kv_indices,
+        dense_page_table,
+        dense_cache_seqlens,
+        sparse_page_table,
+        sparse_cache_seqlens,
+        req_to_token,
+        req_indices,
+        ctx.winfo_q_indices,
+        ctx.winfo_kv_offsets,
+        ctx.winfo_kv_lens,
+        ctx.winfo_num_workloads,
+        ctx.winfo_chunk_size,
+        ctx.page_size,
+        ctx.num_kv_heads,
+        ctx.topk_val,
+        ctx.page_reserved_bos,
+        ctx.page_reserved_eos,
+        ctx.max_chunk_size,
+        ctx.min_chunk_size,
+    )
+    ctx.set_batch_size(cached_seq_lens.shape[0])
 
 
 def chunkwise_nh2hn_transpose(*args, **kwargs):
