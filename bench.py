@@ -26,11 +26,13 @@ Other configurations (side measurements, not the headline):
                      known size), and exits: the program a counter pass
                      (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) profiles.
 
+  --attention        paged decode attention over the sparse table the indexer
+                     selects and over the dense table (all pages), per layer;
   --flow gqa / quest the same decode step with gqa_block_sparse_attention or
                      gqa_quest_sparse_attention (every op launched on its own).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--config c2|c3|c4|c5] [--flow block_sparse|gqa|quest]
+                       [--config c2|c3|c4|c5] [--flow block_sparse|gqa|quest] [--attention]
                        [--layers N] [--traffic-probe]
 """
 from __future__ import annotations
@@ -73,6 +75,8 @@ def _parse():
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"])
     ap.add_argument("--flow", default="block_sparse", choices=sorted(FLOWS),
                     help="registered flow of the decode step (side measurement unless block_sparse)")
+    ap.add_argument("--attention", action="store_true",
+                    help="side measurement: paged decode attention over the sparse and the dense table")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the kernels a counter pass profiles, print their sizes, exit")
     return ap.parse_args()
@@ -403,6 +407,53 @@ def bench_flow(args, dev) -> dict:
     }
 
 
+def bench_attention(args, dev) -> dict:
+    """Side measurement: paged decode attention at C2 shapes over the sparse
+    table (the indexer's selection) and over the dense table (every page)."""
+    from vortex_torch import _hip
+    from vortex_torch.decode_attention import dense_decode_attention, sparse_decode_attention
+    from vortex_torch.indexer.utils_sglang import plan_decode
+
+    batch = getattr(W, args.config)()
+    H, G, D, P, B = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size, batch.batch
+    ic, _ = W.make_contexts(batch, dev)
+    db = batch.to(dev)
+    plan_decode(db.seq_lens, db.req_to_token, db.req_indices, ic)
+    sc = W.randn_bf16((ic.dense_kv_indices.numel(), 1, 1), 5, dev)
+    _hip.topk_select(sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, ic.sparse_kv_indices,
+                     B * H, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+    layers = max(1, min(args.layers, 8))  # per-layer pools, far beyond the Infinity Cache
+    pools = [(W.randn_bf16((batch.pool_pages * H, P, D), 11 + 2 * i, dev),
+              W.randn_bf16((batch.pool_pages * H, P, D), 12 + 2 * i, dev)) for i in range(layers)]
+    q = W.randn_bf16((B * H * G, D), 13, dev)
+    o = torch.empty_like(q)
+    out = {}
+    with torch._C.DisableTorchFunctionSubclass():
+        for name, fn, ip in (("sparse", sparse_decode_attention, ic.sparse_kv_indptr),
+                             ("dense", dense_decode_attention, ic.dense_kv_indptr)):
+            g = capture(lambda: [fn(q, k, v, ic, out=o) for k, v in pools])
+            us = time_graph(g, args.steps, args.warmup) * 1000.0 / layers
+            S = B * H
+            pages = int(ip[S].item())
+            last = ic.kv_last_page_len[:S].to(torch.int64)
+            n_seg = torch.diff(ip[:S + 1].to(torch.int64))
+            tokens = int(((n_seg - 1).clamp(min=0) * P + torch.where(n_seg > 0, last, torch.zeros_like(last))).sum())
+            nbytes = tokens * D * 2 * 2 + pages * 4 + 2 * q.numel() * 2
+            out[name] = {"us_per_layer": round(us, 2), "pages": pages, "tokens": tokens, "bytes": nbytes,
+                         "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+            print(f"[bench] {name} decode attention {us:.2f} us/layer, {out[name]['GBps']} GB/s",
+                  file=sys.stderr, flush=True)
+    frac = out["sparse"]["GBps"] / HBM_PEAK_GBPS
+    return {
+        "metric": "us per layer of paged decode attention over the block table, side measurement",
+        "value": out["sparse"]["us_per_layer"], "unit": "us/layer", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "higher_is_better": False, "dtype": "bf16", "data": "synthetic (seeded)",
+        "config": {"workload": f"{DECODE_CONFIGS[args.config]}; decode attention, sm_scale 1/sqrt(D)"},
+        "sparse": out["sparse"], "dense": out["dense"], "hbm_frac": round(frac, 4),
+        "speedup_sparse_over_dense": round(out["dense"]["us_per_layer"] / out["sparse"]["us_per_layer"], 2),
+    }
+
+
 def traffic_probe(step: DecodeStep, dev) -> dict:
     """Kernels for a counter pass: every layer's fused indexer launch (twice:
     the second pass is the one to read, the first warms the code object and
@@ -512,6 +563,8 @@ def main():
     torch.cuda.set_device(dev)
     if args.config == "c4":
         out = bench_burst(args, dev)
+    elif args.attention:
+        out = bench_attention(args, dev)
     elif args.flow != "block_sparse":
         out = bench_flow(args, dev)
     else:

@@ -375,6 +375,31 @@ int vtx_set_kv_buffer(void* k_cache, void* v_cache, int64_t cache_rows, const vo
                       const void* new_v, const int64_t* loc, int64_t nnz, int32_t num_kv_heads,
                       int32_t head_dim, int32_t elem_bytes, int32_t page_size, void* stream);
 
+/*
+ * Paged decode attention over a block table (the consumer of the sparse
+ * table the indexer builds; given the dense table it is full attention).
+ * Segment s = b * num_kv_heads + h attends to the pages
+ * kv_indices[kv_indptr[s] .. kv_indptr[s+1]) of the K / V pools
+ * ([cache_rows, page_size, head_dim] bf16; entry = page * H + h), every page
+ * full but the last, which holds kv_last_page_len[s] tokens.  Its query heads
+ * q[s * group_size + g, :] ([B * H * G, head_dim] bf16) each get
+ *   o[s * group_size + g, :] = softmax_t(sm_scale * q . K[t]) @ V
+ * in fp32, rounded to bf16; a segment without tokens gets zeros.
+ * No counterpart in the reference, which hands this table to FlashInfer's
+ * paged decode inside its (un-vendored) SGLang fork; the table format is
+ * the one csrc/utils_sglang.cu:123-184 and csrc/topk.cu:56-113 write.
+ * head_dim 64, 128 or 256; group_size 1..8.
+ */
+int vtx_paged_decode_attention(const uint16_t* q, uint16_t* o, const uint16_t* k_cache,
+                               const uint16_t* v_cache, int64_t cache_rows, const int32_t* kv_indptr,
+                               const int32_t* kv_indices, int64_t kv_indices_len,
+                               const int32_t* kv_last_page_len, int32_t batch_size,
+                               int32_t num_kv_heads, int32_t group_size, int32_t head_dim,
+                               int32_t page_size, float sm_scale, void* stream);
+
+/* 1 if vtx_paged_decode_attention handles this head_dim and group size. */
+int vtx_paged_decode_attention_supported(int32_t head_dim, int32_t group_size);
+
 #ifdef __cplusplus
 }
 #endif

@@ -528,3 +528,39 @@ def plan_decode_fa3(seq_lens, req_to_token, req_indices, page_size: int, num_kv_
               "sparse_pt_written": spt_w, "dense_cache_seqlens": dcs.astype(np.int32),
               "sparse_cache_seqlens": scs.astype(np.int32)})
     return r
+
+
+# --------------------------------------------------------------------------
+# A.8 paged decode attention over a block table (the consumer of the sparse
+#     table: FlashInfer's paged decode in the reference's SGLang fork; table
+#     format csrc/utils_sglang.cu:123-184, csrc/topk.cu:56-113)
+# --------------------------------------------------------------------------
+
+
+def paged_decode_attention(q_bits, k_bits, v_bits, kv_indptr, kv_indices, kv_last_page_len, batch_size: int,
+                           num_kv_heads: int, sm_scale: float):
+    """q [B*H*G, D], pools [rows, P, D] (bf16 bits) -> o bits [B*H*G, D]:
+    softmax(sm_scale * q K^T) V in float64 over each segment's tokens (every
+    page full but the last, which holds kv_last_page_len[s] tokens)."""
+    k = bf16_to_f32(k_bits).astype(np.float64)
+    v = bf16_to_f32(v_bits).astype(np.float64)
+    P, D = k.shape[1], k.shape[2]
+    S = int(batch_size) * int(num_kv_heads)
+    q = bf16_to_f32(np.asarray(q_bits).reshape(-1, D)).astype(np.float64)
+    G = q.shape[0] // max(S, 1)
+    out = np.zeros((q.shape[0], D), dtype=np.float64)
+    ip = np.asarray(kv_indptr, dtype=np.int64)
+    idx = np.asarray(kv_indices, dtype=np.int64)
+    last = np.asarray(kv_last_page_len, dtype=np.int64)
+    for s in range(S):
+        pages = idx[ip[s]:ip[s + 1]]
+        if pages.size == 0:
+            continue
+        kk = k[pages].reshape(-1, D)[:(pages.size - 1) * P + int(last[s])]
+        vv = v[pages].reshape(-1, D)[:(pages.size - 1) * P + int(last[s])]
+        if kk.shape[0] == 0:
+            continue
+        sc = q[s * G:(s + 1) * G] @ kk.T * float(np.float32(sm_scale))
+        w = np.exp(sc - sc.max(axis=1, keepdims=True))
+        out[s * G:(s + 1) * G] = (w / w.sum(axis=1, keepdims=True)) @ vv
+    return f32_to_bf16(out.astype(np.float32))

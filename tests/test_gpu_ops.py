@@ -391,3 +391,61 @@ def test_plan_decode_fa3_matches_oracle(gpu, name):
             np.testing.assert_array_equal(g[wm], exp[wm])
             assert (g[~wm] == -5).all()
     assert (_np(ic.kv_last_page_len) == -9).all()
+
+
+def _attn_inputs(batch, dev, G, D, seed):
+    H, P = batch.num_kv_heads, batch.page_size
+    k = W.randn_bf16((batch.pool_pages * H, P, D), seed, dev)
+    v = W.randn_bf16((batch.pool_pages * H, P, D), seed + 1, dev)
+    q = W.randn_bf16((batch.batch * H * G, D), seed + 2, dev)
+    return q, k, v
+
+
+@pytest.mark.parametrize("table", ["dense", "sparse"])
+@pytest.mark.parametrize("name", ["c1", "c2", "r1", "r2", "r6", "r13"])
+def test_decode_attention_matches_oracle(gpu, name, table):
+    from vortex_torch.decode_attention import dense_decode_attention, sparse_decode_attention
+
+    batch, ic, _ = _planned(name, gpu)
+    G, D = 2, 128
+    q, k, v = _attn_inputs(batch, gpu, G, D, 3)
+    if table == "sparse":  # select with topK on random scores first
+        S = batch.batch * batch.num_kv_heads
+        sc = W.randn_bf16((ic.dense_kv_indices.numel(), 1, 1), 4, gpu)
+        _hip.topk_select(sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, ic.sparse_kv_indices,
+                         S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+        o = sparse_decode_attention(q, k, v, ic)
+        ip, idx = ic.sparse_kv_indptr, ic.sparse_kv_indices
+    else:
+        o = dense_decode_attention(q, k, v, ic)
+        ip, idx = ic.dense_kv_indptr, ic.dense_kv_indices
+    exp = O.paged_decode_attention(_bits(q), _bits(k), _bits(v), _np(ip), _np(idx), _np(ic.kv_last_page_len),
+                                   batch.batch, batch.num_kv_heads, 1.0 / np.sqrt(D))
+    np.testing.assert_allclose(_f(_bits(o)), _f(exp), rtol=1e-2, atol=1e-3)
+
+
+@pytest.mark.parametrize("D,G", [(64, 1), (64, 8), (128, 3), (128, 8), (256, 2), (256, 5)])
+def test_decode_attention_head_shapes(gpu, D, G):
+    from vortex_torch.decode_attention import dense_decode_attention
+
+    batch, ic, _ = _planned("r4", gpu)
+    q, k, v = _attn_inputs(batch, gpu, G, D, 7)
+    o = dense_decode_attention(q, k, v, ic, sm_scale=0.05)
+    exp = O.paged_decode_attention(_bits(q), _bits(k), _bits(v), _np(ic.dense_kv_indptr), _np(ic.dense_kv_indices),
+                                   _np(ic.kv_last_page_len), batch.batch, batch.num_kv_heads, 0.05)
+    np.testing.assert_allclose(_f(_bits(o)), _f(exp), rtol=1e-2, atol=1e-3)
+
+
+def test_sparse_attention_equals_dense_when_budget_covers_all(gpu):
+    """With a budget no smaller than any request, the sparse table is the
+    dense one and so is the attention, bit for bit."""
+    from vortex_torch.decode_attention import dense_decode_attention, sparse_decode_attention
+    from vortex_torch.indexer.utils_sglang import plan_decode
+
+    batch = W.c1()
+    batch.topk = 300  # 256 pages per request < topk + bos + eos
+    ic, _ = W.make_contexts(batch, gpu)
+    b = batch.to(gpu)
+    plan_decode(b.seq_lens, b.req_to_token, b.req_indices, ic)
+    q, k, v = _attn_inputs(batch, gpu, 2, 128, 9)
+    assert torch.equal(sparse_decode_attention(q, k, v, ic), dense_decode_attention(q, k, v, ic))

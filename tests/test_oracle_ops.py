@@ -256,3 +256,61 @@ def test_set_kv_buffer_against_loops():
             ev[(pos // P) * H + h, pos % P] = nv[i, h]
     np.testing.assert_array_equal(gk, ek)
     np.testing.assert_array_equal(gv, ev)
+
+
+def _attn_case(seed, P=4, H=2, G=3, D=8, pages=20, B=3):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn((pages * H, P, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((pages * H, P, D), generator=g).to(torch.bfloat16)
+    q = torch.randn((B * H * G, D), generator=g).to(torch.bfloat16)
+    rng = np.random.default_rng(seed)
+    lens, idx = [], []
+    for s in range(B * H):
+        m = int(rng.integers(0, 6))
+        pg = rng.permutation(pages)[:m]
+        idx.extend((pg * H + s % H).tolist())
+        lens.append(m)
+    ip = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    last = rng.integers(1, P + 1, size=B * H).astype(np.int32)
+    return q, k, v, ip, np.asarray(idx, np.int32), last, B, H, G
+
+
+def test_paged_decode_attention_against_sdpa():
+    q, k, v, ip, idx, last, B, H, G = _attn_case(0)
+    P, D = k.shape[1], k.shape[2]
+    scale = 0.37
+    got = O.paged_decode_attention(_bits(q), _bits(k), _bits(v), ip, idx, last, B, H, scale)
+    for s in range(B * H):
+        pages = idx[ip[s]:ip[s + 1]]
+        rows = q[s * G:(s + 1) * G]
+        if pages.size == 0:
+            assert not got[s * G:(s + 1) * G].any()
+            continue
+        n = (pages.size - 1) * P + int(last[s])
+        kk = k[torch.as_tensor(pages, dtype=torch.long)].reshape(-1, D)[:n].double()
+        vv = v[torch.as_tensor(pages, dtype=torch.long)].reshape(-1, D)[:n].double()
+        ref = torch.nn.functional.scaled_dot_product_attention(
+            rows.double()[None], kk[None], vv[None], scale=float(np.float32(scale)))[0]
+        np.testing.assert_array_equal(got[s * G:(s + 1) * G], _bits(ref.float().to(torch.bfloat16)))
+
+
+def test_paged_decode_attention_closed_forms():
+    # one token: the output is its value row; equal keys: the mean of the values
+    q, k, v, ip, idx, last, B, H, G = _attn_case(1, P=4)
+    P = k.shape[1]
+    one_ip = np.arange(B * H + 1, dtype=np.int32)
+    one_idx = np.asarray([s % H for s in range(B * H)], np.int32)  # page 0 of each head
+    ones = np.ones(B * H, np.int32)
+    got = O.paged_decode_attention(_bits(q), _bits(k), _bits(v), one_ip, one_idx, ones, B, H, 1.0)
+    for s in range(B * H):
+        for gq in range(G):
+            np.testing.assert_array_equal(got[s * G + gq], _bits(v[one_idx[s], 0].contiguous()))
+    kc = k.clone()
+    kc[:] = k[0, 0]
+    full = np.full(B * H, P, np.int32)
+    got = O.paged_decode_attention(_bits(q), _bits(kc), _bits(v), ip, idx, full, B, H, 1.0)
+    for s in range(B * H):
+        pages = idx[ip[s]:ip[s + 1]]
+        if pages.size:
+            mean = v[torch.as_tensor(pages, dtype=torch.long)].reshape(-1, k.shape[2]).double().mean(0)
+            np.testing.assert_array_equal(got[s * G], _bits(mean.float().to(torch.bfloat16)))

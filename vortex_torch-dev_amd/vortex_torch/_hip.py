@@ -83,6 +83,11 @@ _SIGNATURES = {
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
     ),
+    "vtx_paged_decode_attention": (
+        [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_paged_decode_attention_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_segment_scan": (
         [_i32, ctypes.c_float, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
@@ -685,3 +690,30 @@ def set_kv_buffer(k_cache, v_cache, new_k, new_v, loc, page_size: int) -> None:
                                    new_v.data_ptr(), loc.data_ptr(), nnz, H, D, new_k.element_size(),
                                    int(page_size), _stream(dev))
     _check(rc, "set_kv_buffer")
+
+
+@_plain_args
+def paged_decode_attention(q, o, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, batch_size: int,
+                           num_kv_heads: int, sm_scale: float) -> None:
+    """o[s*G + g] = softmax(sm_scale * q K^T) V over segment s's pages of the
+    block table; q / o [B*H*G, D] (or [B, H*G, D]) bf16, pools [rows, P, D]."""
+    lib = load_library()
+    dev = _require_gpu(q, o, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len)
+    for t, n in ((q, "q"), (o, "o"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _req(t, torch.bfloat16, n)
+    for t, n in ((kv_indptr, "kv_indptr"), (kv_indices, "kv_indices"), (kv_last_page_len, "kv_last_page_len")):
+        _req(t, torch.int32, n)
+    if k_cache.dim() != 3 or v_cache.shape != k_cache.shape:
+        raise RuntimeError("vortex_torch: k_cache and v_cache must both be [pages * H, page_size, head_dim]")
+    rows, P, D = (int(x) for x in k_cache.shape)
+    B, H = int(batch_size), int(num_kv_heads)
+    if q.numel() % max(B * H * D, 1) != 0 or o.numel() != q.numel():
+        raise RuntimeError("vortex_torch: q and o must hold B * H * G rows of head_dim")
+    G = q.numel() // max(B * H * D, 1)
+    if kv_indptr.numel() < B * H + 1 or kv_last_page_len.numel() < B * H:
+        raise RuntimeError(f"vortex_torch: kv_indptr needs {B * H + 1} and kv_last_page_len {B * H} entries")
+    with _on_device(dev):
+        rc = lib.vtx_paged_decode_attention(q.data_ptr(), o.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), rows,
+                                            kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_indices.numel(),
+                                            kv_last_page_len.data_ptr(), B, H, G, D, P, float(sm_scale), _stream(dev))
+    _check(rc, "paged_decode_attention")
