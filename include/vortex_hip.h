@@ -204,6 +204,42 @@ int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
 /* 1 if vtx_indexer_fused handles this head_dim (64, 128, 256, 512, 576). */
 int vtx_indexer_fused_supported(int32_t head_dim);
 
+/*
+ * Fused indexer step of the GQA flow: GeMM of the group_size query heads
+ * with every middle page's centroid, optional segment softmax per query
+ * head, maximum over the query heads, top-k select — one launch, one
+ * workgroup per segment.  No single counterpart in the reference: it is the
+ * composition of GeMM (mm_bpr, indexer/triton_kernels/matmul_impl.py:6-113),
+ * Softmax (softmax_inplace_r, indexer/triton_kernels/softmax_impl.py:6-112),
+ * Max(dim=2) (reduce_rr, indexer/triton_kernels/reduce_impl.py:8-146) and
+ * topK (csrc/topk.cu:56-203) as gqa_block_sparse_attention chains them
+ * (vortex_torch/flow/algorithms.py:238-352), for a block table built by the
+ * decode planner.  For each segment s < eff_batch_size whose middle range
+ * [indptr[s]+bos, indptr[s+1]-eos) holds more than topk_val pages, at each
+ * of its pages p:
+ *   score[p*G + g] = bf16(q[s*G + g] . y[dense_kv_indices[p]])     (GeMM)
+ *   score[p*G + g] = bf16(softmax_p(score * scale)) if softmax != 0
+ *   aggr[p]        = max_g score[p*G + g]
+ *   sparse_kv_indices[sparse_kv_indptr[s] + bos + i] = i-th best page by aggr
+ * bit for bit what vtx_ragged_gemm, vtx_segment_scan, vtx_ragged_reduce and
+ * vtx_topk_select write for the same inputs.  q: bf16 [q_rows, head_dim]
+ * (q_rows >= eff_batch_size * group_size); y: bf16 [y_rows, head_dim];
+ * score_rows = pages of score ([score_rows, 1, group_size]); aggr_len =
+ * pages of aggr.  group_size 1..8; topk_val <= 4096.
+ */
+int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                          const uint16_t* y, int64_t y_rows, int32_t head_dim,
+                          uint16_t* score, int64_t score_rows, uint16_t* aggr, int64_t aggr_len,
+                          const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                          const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                          int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                          int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                          int32_t reserved_eos, int32_t max_num_pages, int32_t softmax,
+                          float scale, void* stream);
+
+/* 1 if vtx_indexer_gqa_fused handles this head_dim and group size. */
+int vtx_indexer_gqa_fused_supported(int32_t head_dim, int32_t group_size);
+
 /* Reduction kinds (values of the reference's ReduceType, vortex_torch/utils.py:11-16). */
 #define VTX_REDUCE_MEAN 0
 #define VTX_REDUCE_MAX 1

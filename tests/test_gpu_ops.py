@@ -293,7 +293,125 @@ def test_flow_graph_replay_matches_eager(gpu, flow_name):
         assert torch.equal(run.ic.sparse_kv_indices, eager)
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 100),
+# ------------------------------------------------------- fused GQA indexer
+def _gqa_max_flow():
+    """GeMM -> Max(dim=2) -> topK without the softmax (registered once)."""
+    from vortex_torch.cache import Mean as CMean
+    from vortex_torch.flow import registry, vFlow
+    from vortex_torch.indexer import GeMM, Max, topK
+
+    name = "test_gqa_max_only"
+    if not registry.has(name):
+        @registry.register(name)
+        class _GqaMax(vFlow):
+            def __init__(self):
+                super().__init__()
+                self.gemm, self.max_op, self.output_func = GeMM(), Max(dim=2), topK()
+                self.reduction = CMean(dim=1)
+
+            def forward_indexer(self, q, o, cache, ctx):
+                self.output_func(self.max_op(self.gemm(q, cache["centroids"], ctx=ctx), ctx=ctx), o, ctx=ctx)
+
+            def forward_cache(self, cache, loc, ctx):
+                self.reduction(cache["k"], cache["centroids"], loc=loc, ctx=ctx)
+
+            def create_cache(self, page_size, head_dim):
+                return {"centroids": (1, head_dim)}
+    return name
+
+
+def _gqa_case(name):
+    if name.startswith("r"):
+        return W.random_small(int(name[1:]))
+    if name == "g8d64":  # eight query heads per kv head, head_dim 64
+        return W.make_batch([3000, 700, 5000, 40], pool_pages=600, seed=11, num_kv_heads=2, group_size=8,
+                            head_dim=64, topk=17, bos=2, eos=1)
+    if name == "g4d256":
+        return W.make_batch([2500, 4000], pool_pages=500, seed=12, num_kv_heads=3, group_size=4, head_dim=256,
+                            topk=40, bos=1, eos=0)
+    if name == "staged":  # 5998 middle pages, topk 4096: scores staged in global memory, not LDS
+        return W.make_batch([6000, 4500], pool_pages=10600, seed=13, page_size=1, num_kv_heads=1, group_size=8,
+                            head_dim=128, topk=4096, bos=1, eos=1, max_chunk=512, min_chunk=64)
+    return getattr(W, name)()
+
+
+@pytest.mark.parametrize("flow", ["softmax", "max_only"])
+@pytest.mark.parametrize("name", ["c1", "c2", "r3", "r5", "r8", "g8d64", "g4d256", "staged"])
+def test_gqa_fused_equals_unfused(gpu, monkeypatch, flow, name):
+    """The fused GQA kernel writes the same bits as GeMM, Softmax, Max and
+    topK launched one by one: block table, scores (after the softmax) and
+    the maximum over the query heads, at every position the ops cover."""
+    flow_name = "gqa_block_sparse_attention" if flow == "softmax" else _gqa_max_flow()
+    batch = _gqa_case(name)
+    calls = []
+    real = _hip.indexer_gqa_fused
+    monkeypatch.setattr(_hip, "indexer_gqa_fused", lambda *a, **k: (calls.append(1), real(*a, **k)))
+    out = {}
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("VORTEX_FUSE", fuse)
+        run = _Flow(flow_name, batch, gpu)
+        n0 = len(calls)
+        run.ic.sparse_kv_indices.fill_(-1)
+        run.step()
+        torch.cuda.synchronize()
+        out[fuse] = (_np(run.ic.sparse_kv_indices), _bits(run.flow.gemm.output_buffer),
+                     _bits(run.flow.max_op.output_buffer), len(calls) - n0)
+        ic = run.ic
+    assert out["1"][3] == 1 and out["0"][3] == 0, "fused kernel not (only) taken under VORTEX_FUSE=1"
+    cov = np.zeros(ic.dense_kv_indices.numel(), bool)
+    p, _ = O.workload_positions(*_owinfo(ic))
+    cov[p] = True
+    G = batch.group_size
+    np.testing.assert_array_equal(out["1"][0], out["0"][0])
+    np.testing.assert_array_equal(out["1"][1].reshape(-1, G)[cov], out["0"][1].reshape(-1, G)[cov])
+    np.testing.assert_array_equal(out["1"][2].reshape(-1)[cov], out["0"][2].reshape(-1)[cov])
+    if cov.any():
+        assert out["1"][2].reshape(-1)[cov].any()
+
+
+def test_gqa_fused_graph_replay(gpu, monkeypatch):
+    monkeypatch.setenv("VORTEX_FUSE", "1")
+    run = _Flow("gqa_block_sparse_attention", _gqa_case("g8d64"), gpu)
+    run.step()
+    torch.cuda.synchronize()
+    eager = (run.ic.sparse_kv_indices.clone(), run.flow.max_op.output_buffer.clone())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run.step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run.step()
+    for _ in range(3):
+        run.ic.sparse_kv_indices.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(run.ic.sparse_kv_indices, eager[0])
+        assert torch.equal(run.flow.max_op.output_buffer, eager[1])
+
+
+def test_gqa_fused_rejects_bad_arguments(gpu):
+    batch = W.c1()
+    ic, _ = W.make_contexts(batch, gpu)
+    q = torch.zeros((8, 2, 128), dtype=torch.bfloat16, device=gpu)
+    y = torch.zeros((64, 1, 128), dtype=torch.bfloat16, device=gpu)
+    score = torch.zeros((64, 1, 2), dtype=torch.bfloat16, device=gpu)
+    aggr = torch.zeros((64, 1, 1), dtype=torch.bfloat16, device=gpu)
+    args = (ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, ic.sparse_kv_indices)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _hip.indexer_gqa_fused(q[..., :100].contiguous(), y[..., :100].contiguous(), score, aggr, *args,
+                               8, 30, 1, 1, 256)
+    with pytest.raises(RuntimeError, match="query rows"):
+        _hip.indexer_gqa_fused(q[:3], y, score, aggr, *args, 8, 30, 1, 1, 256)
+    with pytest.raises(RuntimeError, match="topk_val"):
+        _hip.indexer_gqa_fused(q, y, score, aggr, *args, 8, 5000, 1, 1, 256)
+    assert not _hip.indexer_gqa_fused_supported(128, 9)
+
+
+@pytest.mark.parametrize("dtype,D",[(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 100),
                                      (torch.bfloat16, 3), (torch.bfloat16, 576)])
 @pytest.mark.parametrize("kind", ["decode", "prefill"])
 def test_set_kv_buffer_matches_oracle(gpu, dtype, D, kind):

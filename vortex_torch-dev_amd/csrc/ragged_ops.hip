@@ -20,6 +20,7 @@
 #include "vtx_device.h"
 #include "vtx_host.h"
 #include "vtx_score.h"
+#include "vtx_segment.h"
 
 #include <cstring>
 
@@ -450,6 +451,7 @@ struct SegArgs {
   int32_t op;
 };
 
+static_assert(kThreads == vtx::kScanThreads, "the segment scan runs the shared column statistics");
 __global__ __launch_bounds__(kThreads) void segment_scan_kernel(SegArgs a) {
   __shared__ float pm[kThreads];
   __shared__ float ps[kThreads];
@@ -471,76 +473,26 @@ __global__ __launch_bounds__(kThreads) void segment_scan_kernel(SegArgs a) {
     const int c = tid % cols;
     const int r0 = tid / cols;
     const bool active = r0 < per_col;
-    // Segments of up to kR pages per thread keep their values in registers
-    // (all loads issued at once, no second read).
-    constexpr int kR = 8;
-    const bool in_regs = cnt <= (long long)per_col * kR;  // uniform
-    float vals[kR];
-    if (in_regs) {
-#pragma unroll
-      for (int k = 0; k < kR; ++k) {
-        const long long r = r0 + (long long)k * per_col;
-        vals[k] = (active && r < cnt) ? vtx::bf16_to_f32(x[r * cols + c]) : 0.f;
-      }
-    }
-    float m = kLow, s = 0.f;
-    auto add = [&](float v) {
-      if (softmax) {
-        const float u = v * a.scale;
-        if (u > m) {
-          s = s * __expf(m - u) + 1.f;
-          m = u;
-        } else {
-          s += __expf(u - m);
-        }
-      } else {
-        s = fmaf(v, v, s);
-      }
-    };
-    if (active) {
-      if (in_regs) {
-#pragma unroll
-        for (int k = 0; k < kR; ++k)
-          if (r0 + (long long)k * per_col < cnt) add(vals[k]);
-      } else {
-        for (long long r = r0; r < cnt; r += per_col) add(vtx::bf16_to_f32(x[r * cols + c]));
-      }
-    }
-    pm[tid] = m;
-    ps[tid] = s;
-    __syncthreads();
-    // Tree merge of a column's per_col partials (thread r0 of the column
-    // absorbs r0 + h at step h): log2(per_col) steps.
-    for (int h = 1; h < per_col; h <<= 1) {
-      if (active && (r0 % (2 * h)) == 0 && r0 + h < per_col) {
-        const int o = (r0 + h) * cols + c;
-        if (softmax) {
-          const float m1 = pm[tid], m2 = pm[o];
-          const float M = fmaxf(m1, m2);
-          ps[tid] = ps[tid] * __expf(m1 - M) + ps[o] * __expf(m2 - M);
-          pm[tid] = M;
-        } else {
-          ps[tid] += ps[o];
-        }
-      }
-      __syncthreads();
-    }
+    float vals[vtx::kScanRegs];
+    bool in_regs;
+    vtx::column_scan_stats([&](long long r, int col) { return vtx::bf16_to_f32(x[r * cols + col]); }, cnt, cols,
+                           a.scale, softmax, pm, ps, vals, in_regs);
     if (!active) return;
     const float M = pm[c], S = ps[c];
     const float norm = fmaxf(sqrtf(S), 1e-12f);
     if (in_regs) {
 #pragma unroll
-      for (int k = 0; k < kR; ++k) {
+      for (int k = 0; k < vtx::kScanRegs; ++k) {
         const long long r = r0 + (long long)k * per_col;
         if (r < cnt) {
-          const float o = softmax ? __expf(vals[k] * a.scale - M) / S : vals[k] / norm;
+          const float o = softmax ? vtx::softmax_value(vals[k], a.scale, M, S) : vals[k] / norm;
           x[r * cols + c] = (uint16_t)vtx::f32_to_bf16(o);
         }
       }
     } else {
       for (long long r = r0; r < cnt; r += per_col) {
         const float v = vtx::bf16_to_f32(x[r * cols + c]);
-        const float o = softmax ? __expf(v * a.scale - M) / S : v / norm;
+        const float o = softmax ? vtx::softmax_value(v, a.scale, M, S) : v / norm;
         x[r * cols + c] = (uint16_t)vtx::f32_to_bf16(o);
       }
     }

@@ -13,6 +13,11 @@ instead of launched:
 * ``topK`` on a deferred GeMV result launches one fused kernel that computes
   the mean, the scores and the selection, writing all three results.
 
+The GQA flow's ``GeMM`` -> ``Softmax`` -> ``Max(dim=2)`` -> ``topK`` chain is
+recorded the same way: GeMM returns its output as a DeferredTensor, Softmax
+and Max join its record while it is the newest one in the scope, and topK on
+the maximum launches the fused GQA kernel.
+
 Anything else materialises first: a torch operation on any vTensor inside the
 scope flushes all pending work (so no input can change under a recorded
 computation), a DeferredTensor used after the scope is already materialised,
@@ -237,3 +242,10 @@ def materialize(t):
     if p is not None:
         p.flush()
     return t
+
+
+def plain(t: torch.Tensor) -> torch.Tensor:
+    """`t` as a plain torch.Tensor over the same storage, without running its
+    subclass hooks (a recorded launch must not flush the scope it runs in)."""
+    with torch._C.DisableTorchFunctionSubclass():
+        return t.as_subclass(torch.Tensor)

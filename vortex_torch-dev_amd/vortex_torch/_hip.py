@@ -61,6 +61,12 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
+    "vtx_indexer_gqa_fused": (
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_indexer_gqa_fused_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_ragged_gemm": (
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
          _vp, _vp],
@@ -552,6 +558,64 @@ def indexer_fused(
             seg_counters.numel() if seg_counters is not None else 0, int(mode),
             _stream(dev))
     _check(rc, "indexer_fused")
+
+
+def indexer_gqa_fused_supported(head_dim: int, group_size: int) -> bool:
+    return bool(load_library().vtx_indexer_gqa_fused_supported(int(head_dim), int(group_size)))
+
+
+@_plain_args
+def indexer_gqa_fused(
+    q: torch.Tensor,
+    y: torch.Tensor,
+    score: torch.Tensor,
+    aggr: torch.Tensor,
+    dense_kv_indptr: torch.Tensor,
+    sparse_kv_indptr: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    sparse_kv_indices: torch.Tensor,
+    eff_batch_size: int,
+    topk_val: int,
+    reserved_bos: int,
+    reserved_eos: int,
+    max_num_pages: int,
+    softmax_scale=None,
+) -> None:
+    """GeMM + segment softmax (unless softmax_scale is None) + max over the
+    query heads + topK of one GQA layer in one launch.
+
+    q: bf16 [S, G, D]; y: centroid pool [rows, 1, D]; score: the GeMM output
+    buffer [pages, 1, G]; aggr: the Max output buffer [pages, 1, 1]; the
+    block tables come from the planner.
+    """
+    lib = load_library()
+    tensors = [q, y, score, aggr, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
+    dev = _require_gpu(*tensors)
+    for t, n in ((q, "q"), (y, "y (centroids)"), (score, "score"), (aggr, "aggr")):
+        _req(t, torch.bfloat16, n)
+    for t, n in ((dense_kv_indptr, "dense_kv_indptr"), (sparse_kv_indptr, "sparse_kv_indptr"),
+                 (dense_kv_indices, "dense_kv_indices"), (sparse_kv_indices, "sparse_kv_indices")):
+        _req(t, torch.int32, n)
+    if q.dim() != 3:
+        raise RuntimeError(f"vortex_torch: GQA indexer expects q [S, G, D], got {tuple(q.shape)}")
+    S, G, D = (int(v) for v in q.shape)
+    if int(y.shape[-1]) != D:
+        raise RuntimeError(f"vortex_torch: GQA indexer head_dim mismatch ({D} vs {int(y.shape[-1])})")
+    if score.numel() % G:
+        raise RuntimeError(f"vortex_torch: GQA score buffer {tuple(score.shape)} is not [pages, 1, {G}]")
+    eff = int(eff_batch_size)
+    if dense_kv_indptr.numel() < eff + 1 or sparse_kv_indptr.numel() < eff + 1:
+        raise RuntimeError(f"vortex_torch: indptr buffers need {eff + 1} entries")
+    with _on_device(dev):
+        rc = lib.vtx_indexer_gqa_fused(
+            q.data_ptr(), S * G, G, y.data_ptr(), y.numel() // D, D,
+            score.data_ptr(), score.numel() // G, aggr.data_ptr(), aggr.numel(),
+            dense_kv_indptr.data_ptr(), sparse_kv_indptr.data_ptr(),
+            dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
+            eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages),
+            0 if softmax_scale is None else 1, float(softmax_scale or 0.0), _stream(dev))
+    _check(rc, "indexer_gqa_fused")
 
 
 # ----------------------------------------------------------------------------

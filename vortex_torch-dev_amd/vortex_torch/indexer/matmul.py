@@ -169,6 +169,98 @@ mm_rrr = _mm(FORMAT.RAGGED, FORMAT.RAGGED)
 mm_rpr = _mm(FORMAT.RAGGED, FORMAT.PAGED)
 
 
+class PendingGemm(_deferred.Pending):
+    """A recorded ``GeMM`` (BATCHED queries x PAGED centroids, one centroid
+    per page) and what follows it in the GQA flow: an in-place ``Softmax`` of
+    its output and a ``Max`` over the query heads.  ``topK`` on the maximum
+    replaces the chain by one fused launch (``vtx_indexer_gqa_fused``);
+    flushed any other way, the recorded launches run in order.
+
+    A follow-on op joins the chain only when the chain is the newest recorded
+    work of the scope, so no other recorded computation can observe its
+    output between the ops."""
+
+    def __init__(self, op: "GeMM", x: torch.Tensor, y: torch.Tensor, ctx: Context):
+        super().__init__()
+        self.op, self.x, self.y, self.ctx = op, x, y, ctx
+        self.softmax: Optional[Tuple[float, Callable[[], None]]] = None  # (scale, launch)
+        self.max_out: Optional[torch.Tensor] = None
+        self.max_run: Optional[Callable[[], None]] = None
+
+    def _newest(self) -> bool:
+        sc = _deferred.current_scope()
+        return sc is not None and bool(sc.pending) and sc.pending[-1] is self and not self.done
+
+    def accepts_softmax(self) -> bool:
+        return self._newest() and self.softmax is None and self.max_out is None
+
+    def accepts_max(self) -> bool:
+        return self._newest() and self.max_out is None
+
+    def add_softmax(self, scale: float, run: Callable[[], None]) -> None:
+        self.softmax = (float(scale), run)
+
+    def add_max(self, out: torch.Tensor, run: Callable[[], None]) -> None:
+        self.max_out, self.max_run = out, run
+
+    def _run(self) -> None:
+        _deferred.materialize(self.x)
+        self.op.impl(self.x, self.y, self.op.output_buffer, self.ctx)
+        if self.softmax is not None:
+            self.softmax[1]()
+        if self.max_run is not None:
+            self.max_run()
+
+    def fuses_with_topk(self, x: torch.Tensor, ctx: Context) -> bool:
+        if self.done or self.max_out is None or ctx is not self.ctx:
+            return False
+        with torch._C.DisableTorchFunctionSubclass():
+            return x.data_ptr() == self.max_out.data_ptr()
+
+    def fuse_with_topk(self, o: torch.Tensor, ctx: Context) -> None:
+        """GeMM + softmax (if recorded) + max + topK into ``o`` in one kernel."""
+        sc = _deferred.current_scope()
+        if sc is not None:  # earlier recorded work runs first, in program order
+            for p in list(sc.pending):
+                if p is self:
+                    break
+                p.flush()
+        _deferred.materialize(self.x)
+        _hip.indexer_gqa_fused(
+            self.x, self.y, self.op.output_buffer, self.max_out,
+            ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
+            ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
+            ctx.page_reserved_eos, ctx.max_num_pages_per_request,
+            softmax_scale=None if self.softmax is None else self.softmax[0])
+        self.done = True
+
+
+def _gemm_fusable(x: torch.Tensor, y: torch.Tensor, ctx: Context) -> bool:
+    """Whether GeMM may wait for the softmax / max / topK that may follow.
+
+    Like GeMV's, the fused kernel walks each segment's middle pages from the
+    block table instead of the workload list, which describe the same pages
+    for a plan_decode block table; the queries must be BATCHED [S, G, D] with
+    one row per segment and one centroid per page."""
+    if _deferred.current_scope() is None or not _deferred.fusion_enabled():
+        return False
+    with torch._C.DisableTorchFunctionSubclass():
+        if not (x.is_cuda and y.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16):
+            return False
+        if x.dim() != 3 or y.dim() != 3 or int(y.shape[1]) != 1 or not x.is_contiguous():
+            return False
+        S, G, D = (int(v) for v in x.shape)
+    try:
+        span = int(ctx.max_num_pages_per_request) - int(ctx.page_reserved_bos) - int(ctx.page_reserved_eos)
+        if span >= 32768 or int(ctx.topk_val) > 4096:
+            return False
+        if S < int(ctx.batch_size) * int(ctx.num_kv_heads):
+            return False
+    except (TypeError, ValueError):
+        return False
+    return _hip.indexer_gqa_fused_supported(D, G)
+
+
 class GeMM(vOp):
     """O[s] = Y[s] X[s]^T per packed position: x [B or S, N_x, K], y [S, N_y, K]
     -> RAGGED [ctx.max_num_pages, N_y, N_x] (reference vortex_torch/indexer/matmul.py:193-398)."""
@@ -212,8 +304,12 @@ class GeMM(vOp):
         assert self.output_buffer is not None, f"{p}output buffer is None; did profile() run?"
         assert x.device == y.device == self.output_buffer.device, (
             f"{p}device mismatch: x={x.device}, y={y.device}, o={self.output_buffer.device}")
+        if self.impl is mm_bpr and _gemm_fusable(x, y, ctx):
+            pending = PendingGemm(self, x, y, ctx)
+            _deferred.current_scope().add(pending)
+            return _deferred.DeferredTensor.make(self.output_buffer, self.output_format, pending)
         self.impl(x, y, self.output_buffer, ctx)
         return self.output_buffer
 
 
-__all__ = ["GeMV", "GeMM", "mv_bpr", "mm_bpr", "mm_rrr", "mm_rpr"]
+__all__ = ["GeMV", "GeMM", "PendingGemm", "mv_bpr", "mm_bpr", "mm_rrr", "mm_rpr"]

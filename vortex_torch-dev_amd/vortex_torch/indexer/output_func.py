@@ -10,7 +10,9 @@ Profile / execute contract follows the reference
 (vortex_torch/indexer/output_func.py:8-235); execute calls ``topk_output``
 with the reference's argument list, which launches the gfx950 select kernel.
 When its input is a GeMV result recorded inside the same forward_indexer, it
-launches the fused mean + GeMV + select kernel instead.
+launches the fused mean + GeMV + select kernel instead; when it is the
+maximum over query heads of a recorded GeMM (the GQA flow), the fused
+GeMM + softmax + max + select kernel.
 """
 from __future__ import annotations
 
@@ -22,7 +24,7 @@ from .. import _deferred
 from .._C import topk_output
 from ..abs import FORMAT, vOp, vTensor
 from .context import Context
-from .matmul import PendingGemv
+from .matmul import PendingGemm, PendingGemv
 
 
 class topK(vOp):
@@ -60,6 +62,9 @@ class topK(vOp):
         pending = _deferred.pending_of(x)
         if self.impl is topk_output and isinstance(pending, PendingGemv) and pending.ctx is ctx:
             pending.fuse_with_topk(o, ctx, self.seg_counters)
+            return o
+        if self.impl is topk_output and isinstance(pending, PendingGemm) and pending.fuses_with_topk(x, ctx):
+            pending.fuse_with_topk(o, ctx)
             return o
         _deferred.materialize(x)
         self.impl(

@@ -12,11 +12,12 @@ from typing import Callable, Dict, Optional, Tuple
 
 import torch
 
-from .. import _hip
+from .. import _deferred, _hip
 from ..abs import FORMAT, as_vtensor, vOp, vTensor
 from ..utils import ReduceType
 from ._walk import ready, winfo
 from .context import Context
+from .matmul import PendingGemm
 
 
 def reduce_rr(x: torch.Tensor, o: torch.Tensor, dim: int, reduce_type: ReduceType, ctx: Context) -> None:
@@ -60,6 +61,13 @@ class Reduce(vOp):
         p = self._prefix()
         assert self.impl is not None, f"{p}execute called before profile() (impl is None)"
         assert self.output_buffer is not None, f"{p}output buffer is None; did profile() run?"
+        pending = _deferred.pending_of(x)
+        if (self.impl is reduce_rr and self.dim == 2 and self.reduce_type == ReduceType.Max
+                and isinstance(pending, PendingGemm) and pending.ctx is ctx and pending.accepts_max()):
+            # max over the query heads of a recorded GeMM: a following topK fuses all of it
+            xp, out, dim, rt = _deferred.plain(x), self.output_buffer, self.dim, self.reduce_type
+            pending.add_max(out, lambda: reduce_rr(xp, out, dim, rt, ctx))
+            return _deferred.DeferredTensor.make(out, self.output_format, pending)
         self.impl(x, self.output_buffer, self.dim, self.reduce_type, ctx)
         return self.output_buffer
 

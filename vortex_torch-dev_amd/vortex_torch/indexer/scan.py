@@ -14,10 +14,11 @@ from typing import Callable, Dict, Optional, Tuple
 
 import torch
 
-from .. import _hip
+from .. import _deferred, _hip
 from ..abs import FORMAT, vOp, vTensor
 from ._walk import ready
 from .context import Context
+from .matmul import PendingGemm
 
 
 def _segments(ctx: Context) -> int:
@@ -69,6 +70,13 @@ class Softmax(_SegmentOp):
     def execute(self, x: torch.Tensor, ctx: Context) -> torch.Tensor:
         p = self._prefix()
         assert self.impl is not None, f"{p}execute called before profile() (impl is None)"
+        pending = _deferred.pending_of(x)
+        if (self.impl is softmax_inplace_r and isinstance(pending, PendingGemm) and pending.ctx is ctx
+                and pending.accepts_softmax()):
+            # joins the recorded GeMM; runs right after it (or inside the fused GQA kernel)
+            xp, dim, scale = _deferred.plain(x), self.dim, self.scale
+            pending.add_softmax(scale, lambda: softmax_inplace_r(xp, dim, scale, ctx))
+            return x
         self.impl(x, self.dim, self.scale, ctx)
         return x
 
