@@ -377,8 +377,9 @@ def bench_decode(args, dev) -> dict:
 
 
 def bench_flow(args, dev) -> dict:
-    """Side measurement: the decode step of another registered flow (every
-    op launched on its own, one HIP graph per step)."""
+    """Side measurement: the decode step of another registered flow, its ops
+    run as the package runs them (GQA: the fused GeMM + softmax + max + top-k
+    kernel; Quest: one launch per op), one HIP graph per step."""
     batch = getattr(W, args.config)()
     name = FLOWS[args.flow]
     print(f"[bench] building {args.config.upper()} step of {name}: {batch.batch} requests, {args.layers} layers",
@@ -391,8 +392,11 @@ def bench_flow(args, dev) -> dict:
     covered = int(plan["winfo_len"].sum())
     seg_n = np.diff(plan["dense_indptr"].astype(np.int64)) - batch.bos - batch.eos
     sel = int((seg_n > batch.topk).sum()) * batch.topk * 4
-    rows_per_page = 2 if args.flow == "quest" else 1  # envelopes max + min, or one centroid
-    per_layer = B * H * G * D * 2 + covered * (rows_per_page * 2 * D + 4 + 2) + sel
+    # per covered page: its row(s) (envelopes max + min, or one centroid), its
+    # page id, and the score outputs (per-head scores + page score, or the page score)
+    rows_per_page = 2 if args.flow == "quest" else 1
+    outs = 2 * G + 2 if args.flow == "gqa" else 2
+    per_layer = B * H * G * D * 2 + covered * (rows_per_page * 2 * D + 4 + outs) + sel
     gbps = per_layer * args.layers / (us_step * 1e-6) / 1e9
     print(f"[bench] {name} step {us_step:.1f} us", file=sys.stderr, flush=True)
     return {

@@ -16,8 +16,9 @@ constexpr int kScanRegs = 8;       // rows a thread keeps in registers
 // Thread t < kScanThreads takes column t % cols and rows t / cols + k * per_col
 // (per_col = kScanThreads / cols), in increasing r: a running maximum
 // (from -1e30) with rescaled sum, or a sum of squares.  The partials are then
-// merged in LDS by a tree (step h: thread row r0 absorbs r0 + h), so the
-// result depends only on (cnt, cols) and the values.  Threads at or past
+// merged in a fixed order — for power-of-two cols <= 64 a butterfly within
+// each wave and the waves in order, else an LDS tree (step h: thread row r0
+// absorbs r0 + h) — so the result depends only on (cnt, cols) and the values.  Threads at or past
 // kScanThreads only take part in the barriers: every thread of the block
 // must call it.  pm / ps: LDS arrays of kScanThreads floats.  When in_regs
 // comes back true, vals[k] holds the thread's row r0 + k * per_col.
@@ -59,6 +60,35 @@ __device__ __forceinline__ void column_scan_stats(ValAt val_at, long long cnt, i
     } else {
       for (long long r = r0; r < cnt; r += per_col) add(val_at(r, c));
     }
+  }
+  auto merge = [&](float& m1, float& s1, float m2, float s2) {
+    if (softmax) {
+      const float M = fmaxf(m1, m2);
+      s1 = s1 * __expf(m1 - M) + s2 * __expf(m2 - M);
+      m1 = M;
+    } else {
+      s1 += s2;
+    }
+  };
+  if ((cols & (cols - 1)) == 0 && cols <= kWave) {
+    // Power-of-two columns: the lanes of a wave that share a column merge by
+    // an xor butterfly (strides cols .. 32), then thread c < cols merges the
+    // waves' partials in wave order — two barriers instead of a tree.
+    for (int d = cols; d < kWave; d <<= 1) merge(m, s, __shfl_xor(m, d, kWave), __shfl_xor(s, d, kWave));
+    const int wave = tid / kWave;
+    if (tid < kScanThreads && (tid % kWave) < cols) {
+      pm[wave * cols + c] = m;
+      ps[wave * cols + c] = s;
+    }
+    __syncthreads();
+    if (tid < cols) {
+      float M = pm[c], S = ps[c];
+      for (int w = 1; w < kScanThreads / kWave; ++w) merge(M, S, pm[w * cols + c], ps[w * cols + c]);
+      pm[c] = M;
+      ps[c] = S;
+    }
+    __syncthreads();
+    return;
   }
   if (tid < kScanThreads) {
     pm[tid] = m;
