@@ -240,6 +240,40 @@ int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
 /* 1 if vtx_indexer_gqa_fused handles this head_dim and group size. */
 int vtx_indexer_gqa_fused_supported(int32_t head_dim, int32_t group_size);
 
+/*
+ * Fused indexer step of the Quest flow: envelope scores of every middle page
+ * for the group_size query heads, maximum over the query heads, top-k select
+ * — one launch, one workgroup per segment.  No single counterpart in the
+ * reference: it is the composition of Multiply twice and Maximum
+ * (elementwise_binary_bpr / _rrr, indexer/triton_kernels/elementwise_binary_impl.py),
+ * Sum(dim=2) and Max(dim=1) (reduce_rr, indexer/triton_kernels/reduce_impl.py:8-146)
+ * and topK (csrc/topk.cu:56-203) as gqa_quest_sparse_attention chains them
+ * (vortex_torch/flow/algorithms.py:356-496), for a block table built by the
+ * decode planner.  For each segment s < eff_batch_size whose middle range
+ * holds more than topk_val pages, at each of its pages p (e = dense[p]):
+ *   sum[p*G + g] = bf16(sum_d max(bf16(q[s*G+g, d] * ymax[e, d]),
+ *                                 bf16(q[s*G+g, d] * ymin[e, d])))
+ *   aggr[p]      = max_g sum[p*G + g]
+ *   sparse_kv_indices[sparse_kv_indptr[s] + bos + i] = i-th best page by aggr
+ * bit for bit what vtx_ragged_binary, vtx_ragged_reduce and vtx_topk_select
+ * write for the same inputs; the [pages, G, D] products are not written.
+ * q: bf16 [q_rows, head_dim] (q_rows >= eff_batch_size * group_size);
+ * ymax, ymin: bf16 [y_rows, head_dim]; sum_rows = pages of sum
+ * ([sum_rows, group_size, 1]); group_size 1..8; topk_val <= 4096.
+ */
+int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                            const uint16_t* ymax, const uint16_t* ymin, int64_t y_rows,
+                            int32_t head_dim, uint16_t* sum, int64_t sum_rows,
+                            uint16_t* aggr, int64_t aggr_len,
+                            const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                            const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                            int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                            int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                            int32_t reserved_eos, int32_t max_num_pages, void* stream);
+
+/* 1 if vtx_indexer_quest_fused handles this head_dim and group size. */
+int vtx_indexer_quest_fused_supported(int32_t head_dim, int32_t group_size);
+
 /* Reduction kinds (values of the reference's ReduceType, vortex_torch/utils.py:11-16). */
 #define VTX_REDUCE_MEAN 0
 #define VTX_REDUCE_MAX 1

@@ -1,0 +1,95 @@
+"""Host logic of the fused Quest chain (no GPU needed): which launches the
+deferral scope issues for the Quest flow, with the kernels replaced by
+recorders.  The GPU tests check the numbers; these check the bookkeeping —
+one fused launch when the intermediates are not read, the intermediates
+computed when something still refers to them, and every op launched on its
+own under VORTEX_FUSE=0."""
+import pytest
+import torch
+
+import workloads as W
+from vortex_torch import _hip
+from vortex_torch.abs import FORMAT, as_vtensor
+from vortex_torch.flow import algorithms, build_vflow, registry
+from vortex_torch.indexer import elementwise_binary as EB
+
+
+@pytest.fixture
+def launches(monkeypatch):
+    log = []
+
+    def rec(name):
+        return lambda *a, **k: log.append(name)
+
+    monkeypatch.setattr(EB, "_quest_operands", lambda x, y, ctx: True)  # CPU tensors stand in
+    monkeypatch.setattr(_hip, "ragged_binary", rec("binary"))
+    monkeypatch.setattr(_hip, "ragged_reduce", rec("reduce"))
+    monkeypatch.setattr(_hip, "indexer_quest_fused", rec("fused"))
+    monkeypatch.setattr(_hip, "topk_select", rec("topk"))
+    return log
+
+
+def _run(flow_name):
+    batch = W.c1()
+    ic, _ = W.make_contexts(batch, "cpu")
+    flow = build_vflow(flow_name)
+    H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+    rows = batch.pool_pages * H
+    cache = {"k": as_vtensor(torch.zeros((rows, P, D), dtype=torch.bfloat16), FORMAT.PAGED)}
+    for name, (r, c) in flow.create_cache(P, D).items():
+        cache[name] = as_vtensor(torch.zeros((rows, r, c), dtype=torch.bfloat16), FORMAT.PAGED)
+    q = as_vtensor(torch.zeros((batch.batch * H, G, D), dtype=torch.bfloat16), FORMAT.BATCHED)
+    o = as_vtensor(ic.sparse_kv_indices.view(-1, 1, 1), FORMAT.RAGGED)
+    ic.profile()
+    flow.forward_indexer(q, o, cache, ic)
+    ic.execute()
+    flow.forward_indexer(q, o, cache, ic)
+    return flow
+
+
+def _keep_flow():
+    name = "test_quest_keep_cpu"
+    if not registry.has(name):
+        @registry.register(name)
+        class _Keep(algorithms.GQAQuestSparseAttention):
+            def forward_indexer(self, q, o, cache, ctx):
+                s_max = self.mul_max(q, cache["max"], ctx=ctx)
+                s_min = self.mul_min(q, cache["min"], ctx=ctx)
+                self.kept = self.maximum_op(s_max, s_min, ctx=ctx)
+                self.output_func(self.max_op(self.sum(self.kept, ctx=ctx), ctx=ctx), o, ctx=ctx)
+    return name
+
+
+def test_quest_chain_is_one_launch(launches):
+    _run("gqa_quest_sparse_attention")
+    assert launches == ["fused"]
+
+
+def test_quest_chain_computes_observed_intermediates(launches):
+    flow = _run(_keep_flow())
+    # the fused kernel first, then the kept maximum (its two products, then itself)
+    assert launches == ["fused", "binary", "binary", "binary"]
+    assert not flow.kept.is_pending
+
+
+def test_quest_chain_unfused(launches, monkeypatch):
+    monkeypatch.setenv("VORTEX_FUSE", "0")
+    _run("gqa_quest_sparse_attention")
+    assert launches == ["binary", "binary", "binary", "reduce", "reduce", "topk"]
+
+
+def test_quest_chain_broken_by_a_read(launches, monkeypatch):
+    """A torch op on an intermediate inside forward_indexer runs the recorded
+    work first; the chain then launches op by op."""
+    name = "test_quest_read_cpu"
+    if not registry.has(name):
+        @registry.register(name)
+        class _Read(algorithms.GQAQuestSparseAttention):
+            def forward_indexer(self, q, o, cache, ctx):
+                s_max = self.mul_max(q, cache["max"], ctx=ctx)
+                s_min = self.mul_min(q, cache["min"], ctx=ctx)
+                s = self.maximum_op(s_max, s_min, ctx=ctx)
+                self.peek = float(s.sum())  # a read
+                self.output_func(self.max_op(self.sum(s, ctx=ctx), ctx=ctx), o, ctx=ctx)
+    _run(name)
+    assert launches == ["binary", "binary", "binary", "reduce", "reduce", "topk"]

@@ -243,7 +243,9 @@ def test_gqa_block_sparse_flow(gpu, name):
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "r3"])
-def test_gqa_quest_flow(gpu, name):
+def test_gqa_quest_flow(gpu, monkeypatch, name):
+    # stage by stage: every op launched on its own writes its output buffer
+    monkeypatch.setenv("VORTEX_FUSE", "0")
     batch = W.random_small(3) if name == "r3" else getattr(W, name)()
     run = _Flow("gqa_quest_sparse_attention", batch, gpu)
     run.step()
@@ -391,6 +393,72 @@ def test_gqa_fused_graph_replay(gpu, monkeypatch):
         torch.cuda.synchronize()
         assert torch.equal(run.ic.sparse_kv_indices, eager[0])
         assert torch.equal(run.flow.max_op.output_buffer, eager[1])
+
+
+def _quest_keep_flow():
+    """The Quest flow that keeps the elementwise maximum alive past forward_indexer."""
+    from vortex_torch.flow import algorithms, registry
+
+    name = "test_quest_keep"
+    if not registry.has(name):
+        @registry.register(name)
+        class _QuestKeep(algorithms.GQAQuestSparseAttention):
+            def forward_indexer(self, q, o, cache, ctx):
+                s_max = self.mul_max(q, cache["max"], ctx=ctx)
+                s_min = self.mul_min(q, cache["min"], ctx=ctx)
+                self.kept = self.maximum_op(s_max, s_min, ctx=ctx)
+                self.output_func(self.max_op(self.sum(self.kept, ctx=ctx), ctx=ctx), o, ctx=ctx)
+    return name
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "r3", "r5", "r8", "g8d64", "g4d256", "staged"])
+def test_quest_fused_equals_unfused(gpu, monkeypatch, name):
+    """The fused Quest kernel writes the same block table, row sums and page
+    maxima as the five separate launches; the unread [pages, G, D]
+    intermediates are not written."""
+    batch = _gqa_case(name)
+    calls = []
+    real = _hip.indexer_quest_fused
+    monkeypatch.setattr(_hip, "indexer_quest_fused", lambda *a, **k: (calls.append(1), real(*a, **k)))
+    out = {}
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("VORTEX_FUSE", fuse)
+        run = _Flow("gqa_quest_sparse_attention", batch, gpu)
+        n0 = len(calls)
+        run.ic.sparse_kv_indices.fill_(-1)
+        run.flow.mul_max.output_buffer.fill_(SENTINEL)
+        run.step()
+        torch.cuda.synchronize()
+        out[fuse] = (_np(run.ic.sparse_kv_indices), _bits(run.flow.sum.output_buffer),
+                     _bits(run.flow.max_op.output_buffer), len(calls) - n0, _bits(run.flow.mul_max.output_buffer))
+        ic = run.ic
+    assert out["1"][3] == 1 and out["0"][3] == 0, "fused kernel not (only) taken under VORTEX_FUSE=1"
+    cov = np.zeros(ic.dense_kv_indices.numel(), bool)
+    p, _ = O.workload_positions(*_owinfo(ic))
+    cov[p] = True
+    G = batch.group_size
+    np.testing.assert_array_equal(out["1"][0], out["0"][0])
+    np.testing.assert_array_equal(out["1"][1].reshape(-1, G)[cov], out["0"][1].reshape(-1, G)[cov])
+    np.testing.assert_array_equal(out["1"][2].reshape(-1)[cov], out["0"][2].reshape(-1)[cov])
+    sentinel = _bits(_sentinel((1,), gpu))[0]
+    assert (out["1"][4] == sentinel).all(), "an elided product was written"
+    if cov.any():
+        assert (out["0"][4].reshape(-1, G * batch.head_dim)[cov] != sentinel).any()
+
+
+def test_quest_fused_keeps_observed_intermediates(gpu, monkeypatch):
+    """An intermediate still referenced after forward_indexer is computed."""
+    batch = W.c1()
+    got = {}
+    for fuse in ("1", "0"):
+        monkeypatch.setenv("VORTEX_FUSE", fuse)
+        run = _Flow(_quest_keep_flow(), batch, gpu)
+        run.flow.maximum_op.output_buffer.fill_(SENTINEL)
+        run.step()
+        torch.cuda.synchronize()
+        got[fuse] = (_bits(run.flow.maximum_op.output_buffer), _np(run.ic.sparse_kv_indices))
+    np.testing.assert_array_equal(got["1"][1], got["0"][1])
+    np.testing.assert_array_equal(got["1"][0], got["0"][0])
 
 
 def test_gqa_fused_rejects_bad_arguments(gpu):

@@ -1,0 +1,223 @@
+// Fused indexer step of the Quest flow for gfx950: the envelope score of
+// every middle page for each of the G query heads, the maximum over the query
+// heads and the top-k select — one launch, one workgroup per segment
+// (request, kv head).
+//
+// For a block table built by the decode planner, at every middle page p of a
+// segment s with more than topk of them, with e = dense[p]:
+//   sum[p, g]  = bf16(sum_d max(bf16(q[s*G+g, d] * ymax[e, d]),
+//                               bf16(q[s*G+g, d] * ymin[e, d])))
+//   aggr[p]    = max_g sum[p, g]
+//   sparse[sparse_indptr[s] + bos + i] = the i-th best page by aggr
+// exactly what Multiply (twice), Maximum, Sum(dim=2), Max(dim=1) and topK
+// write when launched one by one: the row sums use the shared Quest pass
+// (vtx_score.h), whose per-lane column order and xor tree are the row-sum
+// kernel's.  The [pages, G, D] products and their maximum are not written.
+#include "vtx_device.h"
+#include "vtx_host.h"
+#include "vtx_score.h"
+#include "vtx_select.h"
+
+namespace {
+
+struct QuestArgs {
+  const uint16_t* q;     // [segments * G, D]
+  const uint16_t* ymax;  // [y_rows, D]
+  const uint16_t* ymin;  // [y_rows, D]
+  int64_t y_rows;
+  uint16_t* sum;         // [sum_rows, G, 1]
+  int64_t sum_rows;
+  uint16_t* aggr;        // [aggr_len]
+  int64_t aggr_len;
+  const int32_t* dindptr;
+  const int32_t* sindptr;
+  const int32_t* didx;
+  int64_t didx_len;
+  int32_t* sidx;
+  int64_t sidx_len;
+  int32_t segments, G, dim, topk, bos, eos, row_cap;
+};
+
+template <int T, int LPR, int VPL, int kG>
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_fused_kernel(QuestArgs a) {
+  constexpr int kWaves = T / vtx::kWave;
+  constexpr int kRowsPerLoad = vtx::kWave / LPR;
+  // Two rows per position: half the GeMM's pass keeps the loads of a pass in
+  // registers.  The pass size does not change the sums (each is the xor tree
+  // of its LPR lanes' partials whatever the slot layout).
+  constexpr int kPass = VPL == 1 ? 32 : 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ vtx::SelectShared<T> sh;
+
+  const int seg = blockIdx.x;
+  const int lane = vtx::lane_id();
+  const int wave = threadIdx.x / vtx::kWave;
+  const int grp = lane / LPR;
+  const int col = lane % LPR;
+  const int k = a.topk;
+  const int D = a.dim;
+  const int G = a.G;
+
+  const long long start = (long long)a.dindptr[seg] + a.bos;
+  const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
+  const long long obase = (long long)a.sindptr[seg] + a.bos;
+  if (!(k > 0 && n > k) || start < 0 || start + n > a.sum_rows || start + n > a.aggr_len ||
+      start + n > a.didx_len || obase < 0 || obase + k > a.sidx_len)
+    return;  // uniform: the separate ops write nothing for this segment either
+  const bool cached = n <= a.row_cap;
+  uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
+  int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
+  uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
+  vtx::select_init<T>(sel, k, sh);
+  __syncthreads();  // histogram cleared before any wave counts into it
+
+  // ---- scores, page maxima and keys of every middle page
+  const int32_t* dseg = a.didx + start;
+  const uint16_t* qs = a.q + (long long)seg * G * D;
+  long long share = (n + kWaves - 1) / kWaves;
+  share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+  if (share > kPass) share = kPass;
+  for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
+    const int cnt = (int)min(share, n - p0);
+    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
+    int r = -1;
+    float best = -INFINITY;
+    for (int g0 = 0; g0 < G; g0 += kG) {
+      float xs[kG][VPL][8];
+#pragma unroll
+      for (int gg = 0; gg < kG; ++gg)
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          if (g0 + gg < G) {
+            vtx::unpack8(vtx::ld16(qs + (long long)(g0 + gg) * D + (v * LPR + col) * 8), xs[gg][v]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xs[gg][v][e] = 0.f;
+          }
+        }
+      float sc[kG];
+      vtx::quest_pass_multi<LPR, VPL, kPass, kG>(a.ymax, a.ymin, a.y_rows, D, my_row, cnt, xs, grp, col, &r, sc);
+      if (r >= 0) {
+#pragma unroll
+        for (int gg = 0; gg < kG; ++gg) {
+          if (g0 + gg >= G) break;
+          const uint32_t b = vtx::f32_to_bf16(sc[gg]);
+          a.sum[(start + p0 + r) * G + g0 + gg] = (uint16_t)b;
+          best = fmaxf(best, vtx::bf16_to_f32(b));
+        }
+      }
+    }
+    const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
+    if (r >= 0) {
+      const uint32_t ab = vtx::f32_to_bf16(best);
+      const uint32_t key = vtx::score_key(ab);
+      a.aggr[start + p0 + r] = (uint16_t)ab;
+      if (cached) {
+        keys[p0 + r] = (uint16_t)key;
+        rows[p0 + r] = my_rid;
+      }
+      vtx::select_count<T>(key, sh);
+    }
+  }
+  __syncthreads();
+
+  // ---- top-k of the segment
+  if (cached) {
+    vtx::select_topk_counted<T>([&](long long i) { return (uint32_t)keys[i]; }, n, k, sel, sh);
+  } else {
+    const uint16_t* ag = a.aggr + start;
+    vtx::select_topk_counted<T>([&](long long i) { return vtx::score_key(ag[i]); }, n, k, sel, sh);
+  }
+  vtx::select_emit<T>(sel, k, n, [&](int rk, long long pos) { a.sidx[obase + rk] = cached ? rows[pos] : dseg[pos]; });
+}
+
+constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS; the select tables take up to ~6 KB more
+constexpr int kMaxTopk = 4096;
+constexpr int kMaxGroup = 8;
+
+template <int T, int kG>
+int launch_dim(const QuestArgs& a, int grid, size_t lds, hipStream_t s) {
+  switch (a.dim) {
+    case 64: quest_fused_kernel<T, 8, 1, kG><<<grid, T, lds, s>>>(a); break;
+    case 128: quest_fused_kernel<T, 16, 1, kG><<<grid, T, lds, s>>>(a); break;
+    case 256: quest_fused_kernel<(T > 512 ? 512 : T), 16, 2, 1><<<grid, (T > 512 ? 512 : T), lds, s>>>(a); break;
+    // wide rows keep their query slice in registers: fewer threads, no spills
+    case 512: quest_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1><<<grid, (T > 512 ? 512 : T), lds, s>>>(a); break;
+    case 576: quest_fused_kernel<256, 8, 9, 1><<<grid, 256, lds, s>>>(a); break;
+    default: return vtx::fail(VTX_E_INVALID, "indexer_quest_fused: head_dim %d not supported", a.dim);
+  }
+  return vtx::check_launch("indexer_quest_fused");
+}
+
+template <int T>
+int launch_g(const QuestArgs& a, int grid, size_t lds, hipStream_t s) {
+  return a.G >= 2 ? launch_dim<T, 2>(a, grid, lds, s) : launch_dim<T, 1>(a, grid, lds, s);
+}
+
+}  // namespace
+
+extern "C" int vtx_indexer_quest_fused_supported(int32_t head_dim, int32_t group_size) {
+  return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512 || head_dim == 576) &&
+         group_size >= 1 && group_size <= kMaxGroup;
+}
+
+extern "C" int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                                       const uint16_t* ymax, const uint16_t* ymin, int64_t y_rows,
+                                       int32_t head_dim, uint16_t* sum, int64_t sum_rows, uint16_t* aggr,
+                                       int64_t aggr_len, const int32_t* dense_kv_indptr,
+                                       const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+                                       int64_t dense_kv_indices_len, int32_t* sparse_kv_indices,
+                                       int64_t sparse_kv_indices_len, int32_t eff_batch_size, int32_t topk_val,
+                                       int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
+                                       void* stream) {
+  vtx::clear_error();
+  const char* what = "indexer_quest_fused";
+  if (eff_batch_size < 0 || reserved_bos < 0 || reserved_eos < 0)
+    return vtx::fail(VTX_E_INVALID, "%s: negative size", what);
+  if (!vtx_indexer_quest_fused_supported(head_dim, group_size))
+    return vtx::fail(VTX_E_INVALID, "%s: head_dim %d with group size %d not supported", what, head_dim,
+                     group_size);
+  if (topk_val > kMaxTopk) return vtx::fail(VTX_E_INVALID, "%s: topk_val %d exceeds %d", what, topk_val, kMaxTopk);
+  if (q_rows < (long long)eff_batch_size * group_size)
+    return vtx::fail(VTX_E_INVALID, "%s: %lld query rows for %d segments of %d heads", what, (long long)q_rows,
+                     eff_batch_size, group_size);
+  if (eff_batch_size == 0) return VTX_OK;
+  if (!q || !ymax || !ymin || !sum || !aggr || !dense_kv_indptr || !sparse_kv_indptr || !dense_kv_indices ||
+      !sparse_kv_indices)
+    return vtx::fail(VTX_E_INVALID, "%s: null pointer", what);
+  if (y_rows <= 0) return vtx::fail(VTX_E_INVALID, "%s: empty envelope pools", what);
+  if (!vtx::aligned16(q) || !vtx::aligned16(ymax) || !vtx::aligned16(ymin))
+    return vtx::fail(VTX_E_INVALID, "%s: query and envelope rows must be 16-byte aligned", what);
+  QuestArgs a;
+  a.q = q;
+  a.ymax = ymax;
+  a.ymin = ymin;
+  a.y_rows = y_rows;
+  a.sum = sum;
+  a.sum_rows = sum_rows;
+  a.aggr = aggr;
+  a.aggr_len = aggr_len;
+  a.dindptr = dense_kv_indptr;
+  a.sindptr = sparse_kv_indptr;
+  a.didx = dense_kv_indices;
+  a.didx_len = dense_kv_indices_len;
+  a.sidx = sparse_kv_indices;
+  a.sidx_len = sparse_kv_indices_len;
+  a.segments = eff_batch_size;
+  a.G = group_size;
+  a.dim = head_dim;
+  a.topk = topk_val > 0 ? topk_val : 0;
+  a.bos = reserved_bos;
+  a.eos = reserved_eos;
+  const long long want = max_num_pages > 0 ? max_num_pages : 0;
+  const long long room = (kLdsBudget - (long long)a.topk * 8) / 6;  // page id + key per page
+  long long cap = want < room ? want : room;
+  cap &= ~7LL;
+  if (cap < 0) cap = 0;
+  a.row_cap = (int32_t)cap;
+  const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 6;
+  hipStream_t s = vtx::as_stream(stream);
+  if (max_num_pages <= 256) return launch_g<256>(a, eff_batch_size, lds, s);
+  if (max_num_pages <= 1024) return launch_g<512>(a, eff_batch_size, lds, s);
+  return launch_g<1024>(a, eff_batch_size, lds, s);
+}

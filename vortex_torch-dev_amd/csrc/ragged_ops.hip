@@ -77,9 +77,7 @@ __device__ __forceinline__ long long opnd_row(const Opnd& x, const Walk& w, int 
   return (r >= 0 && r < x.rows) ? r : -1;
 }
 
-__device__ __forceinline__ float bf16r(float f) {
-  return vtx::bf16_to_f32(vtx::f32_to_bf16(f));
-}
+using vtx::bf16r;
 
 // ------------------------------------------------------------------ GeMM
 // o[p, c, g] = bf16(fp32 sum_k x[rx, g, k] * y[ry, c, k]); o is

@@ -33,6 +33,9 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   return u >> 16;
 }
 
+// f rounded to the nearest bf16 (ties to even), as an fp32 value.
+__device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
 // Maps a bf16 bit pattern to a 16-bit unsigned key whose unsigned order is
 // the numeric order of the scores; -0.0 and +0.0 map to the same key.
 __device__ __forceinline__ uint32_t score_key(uint32_t bits16) {

@@ -1,6 +1,6 @@
-// The row-scoring pass shared by the fused indexer and the paged GeMM:
-// dot products of kG fp32 query rows with up to kPass gathered bf16 rows,
-// one wave, every row load issued before any arithmetic.
+// The row-scoring passes shared by the fused indexer kernels and the paged
+// GeMM: kG fp32 query rows against up to kPass gathered bf16 rows (or row
+// pairs), one wave, every row load issued before any arithmetic.
 #pragma once
 
 #include "vtx_device.h"
@@ -15,54 +15,60 @@ constexpr int segment_pass() {
 }
 
 // One wave pass over `cnt` <= kPass consecutive positions; lane l (< cnt)
-// holds the l-th position's row id of y ([y_rows, D] bf16) in my_row.  A row
-// is split over LPR lanes x VPL 16-byte vectors (kRowsPerLoad = 64 / LPR rows
-// per wave-wide load, kSlots = kPass / kRowsPerLoad rows per lane); every lane
-// issues its row loads before any arithmetic (kBatch slots at a time for
-// wide rows), then for each query g a reduce-scatter over the LPR lanes
-// leaves each finished score on one lane: sc[g] (fp32, the vtx::dot_row chain
-// of the lane's columns, then an xor tree with strides LPR/2 .. 1), at
-// position *r of the pass; *r = -1 on lanes that own no position.  Rows
-// outside y score 0.
-template <int LPR, int VPL, int kPass, int kG>
-__device__ __forceinline__ void score_pass_multi(const uint16_t* y, long long y_rows, int D, int my_row, int cnt,
-                                                 const float (&xs)[kG][VPL][8], int grp, int col, int* r,
-                                                 float (&sc)[kG]) {
+// holds the l-th position's row id in my_row, naming row my_row of each of
+// the kRows pools ys[] ([y_rows, D] bf16).  A row is split over LPR lanes x
+// VPL 16-byte vectors (kRowsPerLoad = 64 / LPR rows per wave-wide load,
+// kSlots = kPass / kRowsPerLoad rows per lane); every lane issues its row
+// loads before any arithmetic (kBatch slots at a time for wide rows), then
+// part(rows, g) gives the lane's fp32 partial of query g over its columns,
+// and for each query a reduce-scatter over the LPR lanes leaves each finished
+// value on one lane: sc[g] (the partials combined by an xor tree with strides
+// LPR/2 .. 1), at position *r of the pass; *r = -1 on lanes that own no
+// position.  Rows outside the pools give 0.
+template <int LPR, int VPL, int kPass, int kG, int kRows, typename Part>
+__device__ __forceinline__ void row_pass(const uint16_t* const (&ys)[kRows], long long y_rows, int D, int my_row,
+                                         int cnt, int grp, int col, int* r, float (&sc)[kG], Part part) {
   constexpr int kRowsPerLoad = kWave / LPR;
   constexpr int kSlots = kPass / kRowsPerLoad;
-  constexpr int kBatch = VPL <= 2 ? kSlots : (kSlots < 2 ? kSlots : 2);  // slots loaded together
+  constexpr int kWide = kRows == 1 ? (VPL <= 2 ? kSlots : 2) : (VPL == 1 ? 8 : (VPL == 2 ? 4 : 1));
+  constexpr int kBatch = kSlots < kWide ? kSlots : kWide;  // slots loaded together
   static_assert(kSlots >= 1 && kSlots <= LPR && kSlots * kRowsPerLoad == kPass, "pass geometry");
+  static_assert(kSlots % kBatch == 0, "batches must tile the slots");
   int first = __shfl(my_row, 0, kWave);
   if (first < 0 || first >= y_rows) first = 0;
   float acc[kG][kSlots];
 #pragma unroll
   for (int i0 = 0; i0 < kSlots; i0 += kBatch) {
-    U4 buf[kBatch][VPL];
+    U4 buf[kBatch][kRows][VPL];
     bool live[kBatch];
 #pragma unroll
     for (int ii = 0; ii < kBatch; ++ii) {
       const int row = __shfl(my_row, (i0 + ii) * kRowsPerLoad + grp, kWave);
       live[ii] = row >= 0 && row < y_rows;
       if ((i0 + ii) * kRowsPerLoad < cnt) {  // wave-uniform: slots past the pass are skipped
-        const uint16_t* yr = y + (long long)(live[ii] ? row : first) * D;
+        const long long off = (long long)(live[ii] ? row : first) * D;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[ii][v] = ld16_stream(yr + (v * LPR + col) * 8);
+        for (int k = 0; k < kRows; ++k)
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) buf[ii][k][v] = ld16_stream(ys[k] + off + (v * LPR + col) * 8);
       } else {
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[ii][v] = U4{0u, 0u, 0u, 0u};
+        for (int k = 0; k < kRows; ++k)
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) buf[ii][k][v] = U4{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
     for (int ii = 0; ii < kBatch; ++ii)
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
-        const float s = dot_row<VPL>(buf[ii], xs[g]);
+        const float s = part(buf[ii], g);
         acc[g][i0 + ii] = live[ii] ? s : 0.f;
       }
   }
   // Reduce-scatter over the slots (lane keeps slot bits of col from the top),
   // then fold the lanes that still share a slot.  The strides run LPR/2 down
-  // to 1 in both parts.
+  // to 1 in both parts, so each value is the xor-tree sum of its partials.
 #pragma unroll
   for (int g = 0; g < kG; ++g) {
 #pragma unroll
@@ -83,6 +89,43 @@ __device__ __forceinline__ void score_pass_multi(const uint16_t* y, long long y_
   constexpr int kShare = LPR / kSlots;
   const int pos = (col / kShare) * kRowsPerLoad + grp;
   *r = ((col % kShare) == 0 && pos < cnt) ? pos : -1;
+}
+
+// Dot products of kG fp32 query rows with one gathered row per position:
+// the lane's partial is the vtx::dot_row chain over its columns.
+template <int LPR, int VPL, int kPass, int kG>
+__device__ __forceinline__ void score_pass_multi(const uint16_t* y, long long y_rows, int D, int my_row, int cnt,
+                                                 const float (&xs)[kG][VPL][8], int grp, int col, int* r,
+                                                 float (&sc)[kG]) {
+  const uint16_t* const ys[1] = {y};
+  row_pass<LPR, VPL, kPass, kG, 1>(ys, y_rows, D, my_row, cnt, grp, col, r, sc,
+                                   [&](const U4 (&rows)[1][VPL], int g) { return dot_row<VPL>(rows[0], xs[g]); });
+}
+
+// Quest page scores (arXiv:2406.10774) of kG fp32 query rows against each
+// position's key envelope (rows of ymax and ymin):
+//   sum_d max(bf16(q_d * max_d), bf16(q_d * min_d))
+// with the lane's partial summed in column order from 0 — the elementwise
+// multiply, maximum and row-sum kernels' arithmetic, in their order.
+template <int LPR, int VPL, int kPass, int kG>
+__device__ __forceinline__ void quest_pass_multi(const uint16_t* ymax, const uint16_t* ymin, long long y_rows, int D,
+                                                 int my_row, int cnt, const float (&xs)[kG][VPL][8], int grp,
+                                                 int col, int* r, float (&sc)[kG]) {
+  const uint16_t* const ys[2] = {ymax, ymin};
+  row_pass<LPR, VPL, kPass, kG, 2>(ys, y_rows, D, my_row, cnt, grp, col, r, sc,
+                                   [&](const U4 (&rows)[2][VPL], int g) {
+                                     float s = 0.f;
+#pragma unroll
+                                     for (int v = 0; v < VPL; ++v) {
+                                       float mx[8], mn[8];
+                                       unpack8(rows[0][v], mx);
+                                       unpack8(rows[1][v], mn);
+#pragma unroll
+                                       for (int e = 0; e < 8; ++e)
+                                         s += fmaxf(bf16r(xs[g][v][e] * mx[e]), bf16r(xs[g][v][e] * mn[e]));
+                                     }
+                                     return s;
+                                   });
 }
 
 // Single-query form: returns the lane's finished score.

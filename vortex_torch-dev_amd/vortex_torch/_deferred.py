@@ -18,6 +18,15 @@ recorded the same way: GeMM returns its output as a DeferredTensor, Softmax
 and Max join its record while it is the newest one in the scope, and topK on
 the maximum launches the fused GQA kernel.
 
+The Quest flow's two ``Multiply`` -> ``Maximum`` -> ``Sum(dim=2)`` ->
+``Max(dim=1)`` -> ``topK`` chain is recorded op by op (:class:`PendingOp`,
+each naming the recorded work it reads); topK on the maximum launches the
+fused Quest kernel, which writes the row sums, the maximum and the block
+table.  The [pages, G, D] products and their elementwise maximum are then
+*elided*: they are computed only if something reads them — a torch op or
+an indexer op inside the scope, or a tensor still referring to them when
+the scope ends.  An op's ``output_buffer`` read directly is not such a read.
+
 Anything else materialises first: a torch operation on any vTensor inside the
 scope flushes all pending work (so no input can change under a recorded
 computation), a DeferredTensor used after the scope is already materialised,
@@ -30,7 +39,8 @@ from __future__ import annotations
 import contextlib
 import os
 import threading
-from typing import List, Optional
+import weakref
+from typing import Callable, List, Optional
 
 import torch
 
@@ -75,18 +85,43 @@ def fused_layout() -> int:
 
 
 class Pending:
-    """A recorded computation that writes a tensor's storage when flushed."""
+    """A recorded computation that writes a tensor's storage when flushed.
+
+    ``elided`` marks work a fused launch made unnecessary for the flow's
+    results (an intermediate of the fused chain): it still runs when its
+    result is read, and when the scope ends while a tensor still refers to
+    that result; otherwise it is dropped."""
 
     def __init__(self):
         self.done = False
+        self.elided = False
+        self._outs: List[weakref.ref] = []  # the DeferredTensors it produces
 
     def flush(self) -> None:
         if not self.done:
             self.done = True
             self._run()
 
+    def observed(self) -> bool:
+        return any(r() is not None for r in self._outs)
+
     def _run(self) -> None:  # pragma: no cover - subclasses
         raise NotImplementedError
+
+
+class PendingOp(Pending):
+    """A recorded launch of one indexer op (``kind`` names the op and its
+    role, ``info`` holds its plain operands).  The recorded work of its
+    inputs (``deps``) runs first."""
+
+    def __init__(self, kind: str, launch: Callable[[], None], deps: List[Pending], **info):
+        super().__init__()
+        self.kind, self._launch, self.deps, self.info = kind, launch, deps, info
+
+    def _run(self) -> None:
+        for d in self.deps:
+            d.flush()
+        self._launch()
 
 
 class PendingMean(Pending):
@@ -110,7 +145,10 @@ class Scope:
 
     def flush(self) -> None:
         while self.pending:
-            self.pending.pop(0).flush()
+            p = self.pending.pop(0)
+            if p.elided and not p.observed():
+                continue  # superseded by a fused launch and never read
+            p.flush()
 
 
 def current_scope() -> Optional[Scope]:
@@ -195,6 +233,7 @@ def _make_deferred_class():
             out = torch.Tensor._make_subclass(cls, base, require_grad=False)
             out._format = fmt
             out._pending = pending
+            pending._outs.append(weakref.ref(out))
             return out
 
         def materialize(self) -> None:
@@ -246,6 +285,9 @@ def materialize(t):
 
 def plain(t: torch.Tensor) -> torch.Tensor:
     """`t` as a plain torch.Tensor over the same storage, without running its
-    subclass hooks (a recorded launch must not flush the scope it runs in)."""
+    subclass hooks (a recorded launch must not flush the scope it runs in).
+    The result does not keep `t`'s Python object alive (``as_subclass`` would:
+    its view refers back to `t`), so a recorded launch holding it does not
+    make an elided result look observed."""
     with torch._C.DisableTorchFunctionSubclass():
-        return t.as_subclass(torch.Tensor)
+        return torch.Tensor._make_subclass(torch.Tensor, t, require_grad=False)

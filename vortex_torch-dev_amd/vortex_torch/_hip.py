@@ -67,6 +67,12 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_indexer_gqa_fused_supported": ([_i32, _i32], ctypes.c_int),
+    "vtx_indexer_quest_fused": (
+        [_vp, _i64, _i32, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _vp],
+        ctypes.c_int,
+    ),
+    "vtx_indexer_quest_fused_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_ragged_gemm": (
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
          _vp, _vp],
@@ -616,6 +622,65 @@ def indexer_gqa_fused(
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages),
             0 if softmax_scale is None else 1, float(softmax_scale or 0.0), _stream(dev))
     _check(rc, "indexer_gqa_fused")
+
+
+def indexer_quest_fused_supported(head_dim: int, group_size: int) -> bool:
+    return bool(load_library().vtx_indexer_quest_fused_supported(int(head_dim), int(group_size)))
+
+
+@_plain_args
+def indexer_quest_fused(
+    q: torch.Tensor,
+    ymax: torch.Tensor,
+    ymin: torch.Tensor,
+    score: torch.Tensor,
+    aggr: torch.Tensor,
+    dense_kv_indptr: torch.Tensor,
+    sparse_kv_indptr: torch.Tensor,
+    dense_kv_indices: torch.Tensor,
+    sparse_kv_indices: torch.Tensor,
+    eff_batch_size: int,
+    topk_val: int,
+    reserved_bos: int,
+    reserved_eos: int,
+    max_num_pages: int,
+) -> None:
+    """Quest envelope scores + max over the query heads + topK of one layer
+    in one launch.
+
+    q: bf16 [S, G, D]; ymax, ymin: the envelope pools [rows, 1, D]; score:
+    the Sum(dim=2) output buffer [pages, G, 1]; aggr: the Max(dim=1) output
+    buffer [pages, 1, 1]; the block tables come from the planner.
+    """
+    lib = load_library()
+    tensors = [q, ymax, ymin, score, aggr, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices,
+               sparse_kv_indices]
+    dev = _require_gpu(*tensors)
+    for t, n in ((q, "q"), (ymax, "ymax"), (ymin, "ymin"), (score, "score"), (aggr, "aggr")):
+        _req(t, torch.bfloat16, n)
+    for t, n in ((dense_kv_indptr, "dense_kv_indptr"), (sparse_kv_indptr, "sparse_kv_indptr"),
+                 (dense_kv_indices, "dense_kv_indices"), (sparse_kv_indices, "sparse_kv_indices")):
+        _req(t, torch.int32, n)
+    if q.dim() != 3:
+        raise RuntimeError(f"vortex_torch: Quest indexer expects q [S, G, D], got {tuple(q.shape)}")
+    S, G, D = (int(v) for v in q.shape)
+    if int(ymax.shape[-1]) != D or tuple(ymax.shape) != tuple(ymin.shape):
+        raise RuntimeError(f"vortex_torch: Quest envelope pools {tuple(ymax.shape)} / {tuple(ymin.shape)} "
+                           f"do not match head_dim {D}")
+    if score.numel() % G:
+        raise RuntimeError(f"vortex_torch: Quest score buffer {tuple(score.shape)} is not [pages, {G}, 1]")
+    eff = int(eff_batch_size)
+    if dense_kv_indptr.numel() < eff + 1 or sparse_kv_indptr.numel() < eff + 1:
+        raise RuntimeError(f"vortex_torch: indptr buffers need {eff + 1} entries")
+    with _on_device(dev):
+        rc = lib.vtx_indexer_quest_fused(
+            q.data_ptr(), S * G, G, ymax.data_ptr(), ymin.data_ptr(), ymax.numel() // D, D,
+            score.data_ptr(), score.numel() // G, aggr.data_ptr(), aggr.numel(),
+            dense_kv_indptr.data_ptr(), sparse_kv_indptr.data_ptr(),
+            dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
+            sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
+            eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), _stream(dev))
+    _check(rc, "indexer_quest_fused")
 
 
 # ----------------------------------------------------------------------------

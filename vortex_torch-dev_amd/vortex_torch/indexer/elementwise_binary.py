@@ -14,7 +14,7 @@ from typing import Callable, Dict, Optional, Tuple
 
 import torch
 
-from .. import _hip
+from .. import _deferred, _hip
 from ..abs import FORMAT, as_vtensor, vOp, vTensor
 from ..utils import ElementwiseBinaryOpType
 from ._walk import ROW_MODE, ready, winfo
@@ -80,8 +80,62 @@ class Elementwise_Binary(vOp):
         assert self.output_buffer is not None, f"{p}output buffer is None; did profile() run?"
         assert x.device == y.device == self.output_buffer.device, (
             f"{p}device mismatch: x={x.device}, y={y.device}, o={self.output_buffer.device}")
+        kind = self._quest_role(x, y, ctx)
+        if kind is not None:
+            return self._record(kind, x, y, ctx)
         self.impl(x, y, self.output_buffer, self.op_type, self.alpha, self.beta, ctx)
         return self.output_buffer
+
+    # -- recording for the fused Quest kernel (see vortex_torch/_deferred.py)
+    def _quest_role(self, x, y, ctx: Context) -> Optional[str]:
+        """"quest_mul" for q x envelope products, "quest_max" for the maximum
+        of two recorded products of the same queries; None otherwise."""
+        if _deferred.current_scope() is None or not _deferred.fusion_enabled():
+            return None
+        if self.op_type == ElementwiseBinaryOpType.Mul and self.impl is elementwise_binary_bpr:
+            return "quest_mul" if _quest_operands(x, y, ctx) else None
+        if self.op_type == ElementwiseBinaryOpType.Maximum and self.impl is elementwise_binary_rrr:
+            pa, pb = _deferred.pending_of(x), _deferred.pending_of(y)
+            if (isinstance(pa, _deferred.PendingOp) and isinstance(pb, _deferred.PendingOp) and pa is not pb
+                    and pa.kind == pb.kind == "quest_mul" and pa.info["ctx"] is ctx and pb.info["ctx"] is ctx
+                    and not pa.elided and not pb.elided):
+                with torch._C.DisableTorchFunctionSubclass():
+                    same_q = pa.info["x"].data_ptr() == pb.info["x"].data_ptr()
+                    same_y = pa.info["y"].shape == pb.info["y"].shape
+                if same_q and same_y:
+                    return "quest_max"
+        return None
+
+    def _record(self, kind: str, x, y, ctx: Context):
+        xp, yp, out = _deferred.plain(x), _deferred.plain(y), self.output_buffer
+        deps = [d for d in (_deferred.pending_of(x), _deferred.pending_of(y)) if d is not None]
+        op_type, alpha, beta, impl = self.op_type, self.alpha, self.beta, self.impl
+        pending = _deferred.PendingOp(kind, lambda: impl(xp, yp, out, op_type, alpha, beta, ctx), deps,
+                                      x=xp, y=yp, ctx=ctx)
+        _deferred.current_scope().add(pending)
+        return _deferred.DeferredTensor.make(out, self.output_format, pending)
+
+
+def _quest_operands(x, y, ctx: Context) -> bool:
+    """Queries [S, G, D] (BATCHED) times a per-page envelope pool [rows, 1, D]
+    (PAGED), both bf16 on the GPU, in a shape the fused Quest kernel takes."""
+    with torch._C.DisableTorchFunctionSubclass():
+        if not (x.is_cuda and y.is_cuda and x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16):
+            return False
+        if x.dim() != 3 or y.dim() != 3 or int(y.shape[1]) != 1 or int(x.shape[2]) != int(y.shape[2]):
+            return False
+        if not (x.is_contiguous() and y.is_contiguous()):
+            return False
+        S, G, D = (int(v) for v in x.shape)
+    try:
+        span = int(ctx.max_num_pages_per_request) - int(ctx.page_reserved_bos) - int(ctx.page_reserved_eos)
+        if span >= 32768 or int(ctx.topk_val) > 4096:
+            return False
+        if S < int(ctx.batch_size) * int(ctx.num_kv_heads):
+            return False
+    except (TypeError, ValueError):
+        return False
+    return _hip.indexer_quest_fused_supported(D, G)
 
 
 class Maximum(Elementwise_Binary):

@@ -20,7 +20,7 @@ from typing import Callable, Dict, Optional
 
 import torch
 
-from .. import _deferred
+from .. import _deferred, _hip
 from .._C import topk_output
 from ..abs import FORMAT, vOp, vTensor
 from .context import Context
@@ -66,6 +66,9 @@ class topK(vOp):
         if self.impl is topk_output and isinstance(pending, PendingGemm) and pending.fuses_with_topk(x, ctx):
             pending.fuse_with_topk(o, ctx)
             return o
+        if self.impl is topk_output and _quest_chain(pending, ctx) is not None:
+            _fuse_quest(_quest_chain(pending, ctx), o, ctx)
+            return o
         _deferred.materialize(x)
         self.impl(
             x,
@@ -80,6 +83,43 @@ class topK(vOp):
             ctx.max_num_pages_per_request,
         )
         return o
+
+
+def _quest_chain(aggr, ctx: Context):
+    """(mul_a, mul_b, maximum, row sum, page maximum) recorded for the fused
+    Quest kernel and ending in `aggr`, or None."""
+    if not (isinstance(aggr, _deferred.PendingOp) and aggr.kind == "quest_aggr" and not aggr.done
+            and aggr.info.get("ctx") is ctx):
+        return None
+    rsum = aggr.deps[0]
+    mx = rsum.deps[0]
+    pa, pb = mx.deps
+    chain = (pa, pb, mx, rsum, aggr)
+    if any(p.done or p.elided for p in chain):
+        return None
+    return chain
+
+
+def _fuse_quest(chain, o: torch.Tensor, ctx: Context) -> None:
+    """Runs the Quest chain's row sums, page maxima and top-k as one kernel;
+    the products and their maximum become elided work."""
+    pa, pb, mx, rsum, aggr = chain
+    sc = _deferred.current_scope()
+    if sc is not None:  # earlier recorded work runs first, in program order
+        for p in list(sc.pending):
+            if p is pa or p is pb:
+                break
+            p.flush()
+    for d in pa.deps + pb.deps:  # recorded producers of q and the envelopes
+        d.flush()
+    _hip.indexer_quest_fused(
+        pa.info["x"], pa.info["y"], pb.info["y"], rsum.info["out"], aggr.info["out"],
+        ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
+        ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
+        ctx.page_reserved_eos, ctx.max_num_pages_per_request)
+    rsum.done = aggr.done = True
+    for p in (pa, pb, mx):
+        p.elided = True
 
 
 __all__ = ["topK"]

@@ -62,6 +62,13 @@ class Reduce(vOp):
         assert self.impl is not None, f"{p}execute called before profile() (impl is None)"
         assert self.output_buffer is not None, f"{p}output buffer is None; did profile() run?"
         pending = _deferred.pending_of(x)
+        role = _quest_role(self, pending, ctx)
+        if role is not None:
+            # the row sum / page maximum of the Quest chain: a following topK fuses it
+            xp, out, dim, rt = _deferred.plain(x), self.output_buffer, self.dim, self.reduce_type
+            rec = _deferred.PendingOp(role, lambda: reduce_rr(xp, out, dim, rt, ctx), [pending], ctx=ctx, out=out)
+            _deferred.current_scope().add(rec)
+            return _deferred.DeferredTensor.make(out, self.output_format, rec)
         if (self.impl is reduce_rr and self.dim == 2 and self.reduce_type == ReduceType.Max
                 and isinstance(pending, PendingGemm) and pending.ctx is ctx and pending.accepts_max()):
             # max over the query heads of a recorded GeMM: a following topK fuses all of it
@@ -70,6 +77,20 @@ class Reduce(vOp):
             return _deferred.DeferredTensor.make(out, self.output_format, pending)
         self.impl(x, self.output_buffer, self.dim, self.reduce_type, ctx)
         return self.output_buffer
+
+
+def _quest_role(op: Reduce, pending, ctx: Context):
+    """"quest_sum" for Sum(dim=2) of a recorded Quest maximum, "quest_aggr" for
+    Max(dim=1) of a recorded Quest row sum; None otherwise."""
+    if op.impl is not reduce_rr or not isinstance(pending, _deferred.PendingOp) or pending.elided:
+        return None
+    if pending.info.get("ctx") is not ctx:
+        return None
+    if pending.kind == "quest_max" and op.dim == 2 and op.reduce_type == ReduceType.Sum:
+        return "quest_sum"
+    if pending.kind == "quest_sum" and op.dim == 1 and op.reduce_type == ReduceType.Max:
+        return "quest_aggr"
+    return None
 
 
 class Max(Reduce):
