@@ -431,6 +431,18 @@ int vtx_segment_scan(int32_t op, float scale, uint16_t* x, int64_t x_rows, int32
                      int32_t reserved_bos, int32_t reserved_eos, void* stream);
 
 /*
+ * Self-check of the device's bf16 rounding; no counterpart in the reference.
+ * Every kernel rounds fp32 to bf16 with gfx950's conversion instruction; this
+ * compares it, over all 2^32 fp32 bit patterns, with the integer
+ * round-to-nearest-even formulation the oracle uses, and adds to the device
+ * counters counts[0] the non-NaN inputs (conversion to bits, and rounding
+ * back to fp32, checked separately) whose result differs, and to counts[1]
+ * the NaN inputs whose bits are not 0x7fc0 or whose fp32 rounding is not a
+ * NaN.  Both stay 0 on a conforming device.  Takes a few milliseconds.
+ */
+int vtx_bf16_rounding_check(unsigned long long* counts, void* stream);
+
+/*
  * Writes new keys and values into the paged pools: for token i < nnz and
  * kv head h, with pos = loc[i], pool row
  *   (pos / page_size) * (page_size * H) + h * page_size + pos % page_size

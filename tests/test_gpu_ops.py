@@ -70,6 +70,13 @@ def _close(got_bits, exp_bits, covered, rtol=1e-2, atol=1e-3):
 LAYOUTS = ["c1", "c2", "c5", "r3", "r11"]
 
 
+def test_bf16_rounding_matches_rne_for_every_input(gpu):
+    """The kernels round fp32 to bf16 with gfx950's conversion instruction;
+    every bit-exact claim against the oracle rests on it being the integer
+    round-to-nearest-even of the oracle for all 2^32 inputs (NaN -> 0x7fc0)."""
+    assert _hip.bf16_rounding_check(gpu) == (0, 0)
+
+
 @pytest.mark.parametrize("name", LAYOUTS)
 def test_gemm_bpr_matches_oracle(gpu, name):
     batch, ic, _ = _planned(name, gpu)

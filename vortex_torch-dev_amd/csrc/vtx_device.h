@@ -23,18 +23,25 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) {
   return __uint_as_float(w & 0xffff0000u);
 }
 
-// fp32 -> bf16 with round-to-nearest-even (the integer-add formulation:
-// add 0x7fff plus the lowest kept bit, truncate).  Every NaN becomes the
-// quiet NaN 0x7fc0, as in torch's conversion.
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+// fp32 -> bf16 with round-to-nearest-even, by gfx950's conversion
+// instruction (v_cvt_pk_bf16_f32).  For every non-NaN input it gives the bits
+// of the integer formulation (add 0x7fff plus the lowest kept bit, truncate)
+// — vtx_bf16_rounding_check compares the two over all 2^32 inputs.  Every
+// NaN becomes the quiet NaN 0x7fc0, as in torch's conversion.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne_int(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
   u += 0x7fffu + ((u >> 16) & 1u);
   return u >> 16;
 }
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  if (__builtin_isnan(f)) return 0x7fc0u;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
 
-// f rounded to the nearest bf16 (ties to even), as an fp32 value.
-__device__ __forceinline__ float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// f rounded to the nearest bf16 (ties to even), as an fp32 value; a NaN
+// stays a NaN (its payload is not specified).
+__device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
 
 // Maps a bf16 bit pattern to a 16-bit unsigned key whose unsigned order is
 // the numeric order of the scores; -0.0 and +0.0 map to the same key.

@@ -106,7 +106,10 @@ __device__ __forceinline__ void score_pass_multi(const uint16_t* y, long long y_
 // position's key envelope (rows of ymax and ymin):
 //   sum_d max(bf16(q_d * max_d), bf16(q_d * min_d))
 // with the lane's partial summed in column order from 0 — the elementwise
-// multiply, maximum and row-sum kernels' arithmetic, in their order.
+// multiply, maximum and row-sum kernels' arithmetic, in their order.  The
+// maximum is taken before the rounding: rounding is monotonic, so
+// bf16(max(a, b)) = max(bf16(a), bf16(b)) for all a, b (a NaN product is
+// dropped by the maximum either way), with one conversion instead of two.
 template <int LPR, int VPL, int kPass, int kG>
 __device__ __forceinline__ void quest_pass_multi(const uint16_t* ymax, const uint16_t* ymin, long long y_rows, int D,
                                                  int my_row, int cnt, const float (&xs)[kG][VPL][8], int grp,
@@ -122,7 +125,7 @@ __device__ __forceinline__ void quest_pass_multi(const uint16_t* ymax, const uin
                                        unpack8(rows[1][v], mn);
 #pragma unroll
                                        for (int e = 0; e < 8; ++e)
-                                         s += fmaxf(bf16r(xs[g][v][e] * mx[e]), bf16r(xs[g][v][e] * mn[e]));
+                                         s += bf16r(fmaxf(xs[g][v][e] * mx[e], xs[g][v][e] * mn[e]));
                                      }
                                      return s;
                                    });

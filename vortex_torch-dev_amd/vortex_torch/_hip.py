@@ -100,6 +100,7 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_paged_decode_attention_supported": ([_i32, _i32], ctypes.c_int),
+    "vtx_bf16_rounding_check": ([_vp, _vp], ctypes.c_int),
     "vtx_segment_scan": (
         [_i32, ctypes.c_float, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
@@ -846,3 +847,16 @@ def paged_decode_attention(q, o, k_cache, v_cache, kv_indptr, kv_indices, kv_las
                                             kv_indptr.data_ptr(), kv_indices.data_ptr(), kv_indices.numel(),
                                             kv_last_page_len.data_ptr(), B, H, G, D, P, float(sm_scale), _stream(dev))
     _check(rc, "paged_decode_attention")
+
+
+def bf16_rounding_check(device="cuda") -> tuple:
+    """(non-NaN mismatches, NaN mismatches) of the device's bf16 rounding
+    against the integer round-to-nearest-even formulation, over all fp32
+    inputs; both are 0 on a conforming device.  Synchronises (a test helper)."""
+    lib = load_library()
+    counts = torch.zeros(2, dtype=torch.int64, device=device)
+    dev = _require_gpu(counts)
+    with _on_device(dev):
+        _check(lib.vtx_bf16_rounding_check(counts.data_ptr(), _stream(dev)), "bf16_rounding_check")
+    c = counts.cpu()
+    return int(c[0]), int(c[1])
