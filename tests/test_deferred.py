@@ -11,6 +11,7 @@ import workloads as W
 from vortex_torch import _hip
 from vortex_torch.abs import FORMAT, as_vtensor
 from vortex_torch.flow import algorithms, build_vflow, registry
+from vortex_torch.cache import reduce as CR
 from vortex_torch.indexer import elementwise_binary as EB
 
 
@@ -22,16 +23,19 @@ def launches(monkeypatch):
         return lambda *a, **k: log.append(name)
 
     monkeypatch.setattr(EB, "_quest_operands", lambda x, y, ctx: True)  # CPU tensors stand in
+    monkeypatch.setattr(CR, "_recordable_operands", lambda x, out, loc: True)
     monkeypatch.setattr(_hip, "ragged_binary", rec("binary"))
     monkeypatch.setattr(_hip, "ragged_reduce", rec("reduce"))
     monkeypatch.setattr(_hip, "indexer_quest_fused", rec("fused"))
     monkeypatch.setattr(_hip, "topk_select", rec("topk"))
+    monkeypatch.setattr(_hip, "page_reduce", rec("page_reduce"))
+    monkeypatch.setattr(_hip, "page_reduce_multi", lambda x, outs, *a, **k: log.append(f"page_reduce_multi{len(outs)}"))
     return log
 
 
-def _run(flow_name):
+def _run(flow_name, cache_step=False, indexer=True):
     batch = W.c1()
-    ic, _ = W.make_contexts(batch, "cpu")
+    ic, cc = W.make_contexts(batch, "cpu")
     flow = build_vflow(flow_name)
     H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
     rows = batch.pool_pages * H
@@ -40,10 +44,17 @@ def _run(flow_name):
         cache[name] = as_vtensor(torch.zeros((rows, r, c), dtype=torch.bfloat16), FORMAT.PAGED)
     q = as_vtensor(torch.zeros((batch.batch * H, G, D), dtype=torch.bfloat16), FORMAT.BATCHED)
     o = as_vtensor(ic.sparse_kv_indices.view(-1, 1, 1), FORMAT.RAGGED)
+    loc = torch.arange(batch.batch, dtype=torch.int64) * P + P - 1
     ic.profile()
+    cc.profile()
+    flow.forward_cache(cache, loc, cc)
     flow.forward_indexer(q, o, cache, ic)
     ic.execute()
-    flow.forward_indexer(q, o, cache, ic)
+    cc.execute()
+    if cache_step:
+        flow.forward_cache(cache, loc, cc)
+    if indexer:
+        flow.forward_indexer(q, o, cache, ic)
     return flow
 
 
@@ -93,3 +104,20 @@ def test_quest_chain_broken_by_a_read(launches, monkeypatch):
                 self.output_func(self.max_op(self.sum(s, ctx=ctx), ctx=ctx), o, ctx=ctx)
     _run(name)
     assert launches == ["binary", "binary", "binary", "reduce", "reduce", "topk"]
+
+
+def test_quest_cache_reductions_are_one_pass(launches):
+    """forward_cache's CMax and CMin of the same pool and loc: one launch."""
+    _run("gqa_quest_sparse_attention", cache_step=True)
+    assert launches == ["page_reduce_multi2", "fused"]
+
+
+def test_quest_cache_reductions_unfused(launches, monkeypatch):
+    monkeypatch.setenv("VORTEX_FUSE", "0")
+    _run("gqa_quest_sparse_attention", cache_step=True)
+    assert launches[:2] == ["page_reduce", "page_reduce"]
+
+
+def test_single_cache_reduction_stays_single(launches):
+    _run("gqa_block_sparse_attention", cache_step=True, indexer=False)
+    assert launches == ["page_reduce"]

@@ -437,8 +437,12 @@ def test_quest_fused_equals_unfused(gpu, monkeypatch, name):
         run.step()
         torch.cuda.synchronize()
         out[fuse] = (_np(run.ic.sparse_kv_indices), _bits(run.flow.sum.output_buffer),
-                     _bits(run.flow.max_op.output_buffer), len(calls) - n0, _bits(run.flow.mul_max.output_buffer))
+                     _bits(run.flow.max_op.output_buffer), len(calls) - n0, _bits(run.flow.mul_max.output_buffer),
+                     _bits(run.cache["max"]), _bits(run.cache["min"]))
         ic = run.ic
+    # forward_cache: CMax + CMin as one pass (fused) equal the two launches
+    np.testing.assert_array_equal(out["1"][5], out["0"][5])
+    np.testing.assert_array_equal(out["1"][6], out["0"][6])
     assert out["1"][3] == 1 and out["0"][3] == 0, "fused kernel not (only) taken under VORTEX_FUSE=1"
     cov = np.zeros(ic.dense_kv_indices.numel(), bool)
     p, _ = O.workload_positions(*_owinfo(ic))

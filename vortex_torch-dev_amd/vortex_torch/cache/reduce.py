@@ -13,6 +13,11 @@ Profile / execute contract follows the reference
 (PAGED, PAGED) — the one flows use on the cache path; it runs the gfx950
 kernel ``vtx_page_reduce``.  :class:`MultiReduce` is an addition: several
 reductions of the same pool in one pass over it.
+
+Inside a flow's execute-mode ``forward_cache`` the reductions are recorded
+and consecutive ones over the same pool and ``loc`` (the Quest flow's CMax
+and CMin) run as one such pass when the method returns, or earlier when
+torch reads one of their outputs; ``VORTEX_FUSE=0`` launches each at once.
 """
 from __future__ import annotations
 
@@ -20,7 +25,7 @@ from typing import Callable, Dict, Optional, Sequence, Tuple
 
 import torch
 
-from .. import _hip
+from .. import _deferred, _hip
 from ..abs import FORMAT, as_vtensor, vOp, vTensor
 from ..utils import ReduceType
 from .context import Context
@@ -43,6 +48,63 @@ def reduce_pp(x: torch.Tensor, output: torch.Tensor, loc: torch.Tensor, ctx: Con
               reduce_type: ReduceType) -> None:
     """(PAGED x, PAGED output): page-finish reduction triggered by loc."""
     _hip.page_reduce(x, output, loc, ctx.head_num, ctx.page_size, dim, _kernel_type(reduce_type))
+
+
+class _PendingPageReduce(_deferred.Pending):
+    """Page-finish reductions of one pool for one loc, recorded inside a
+    flow's forward_cache: consecutive ones (up to four) run as one pass over
+    the finished tiles (``vtx_page_reduce_multi``), whose outputs equal the
+    separate launches' bit for bit."""
+
+    MAX_OUTPUTS = 4
+
+    def __init__(self, x: torch.Tensor, loc: torch.Tensor, ctx: Context, dim: int):
+        super().__init__()
+        self.x, self.loc, self.ctx, self.dim = x, loc, ctx, dim
+        self.outs, self.types = [], []
+
+    def accepts(self, x: torch.Tensor, out: torch.Tensor, loc: torch.Tensor, ctx: Context, dim: int) -> bool:
+        if self.done or ctx is not self.ctx or dim != self.dim or len(self.outs) >= self.MAX_OUTPUTS:
+            return False
+        ptr = out.data_ptr()
+        return (x.data_ptr() == self.x.data_ptr() and x.shape == self.x.shape and loc.data_ptr() == self.loc.data_ptr()
+                and loc.numel() == self.loc.numel() and all(o.data_ptr() != ptr for o in self.outs))
+
+    def add(self, out: torch.Tensor, kernel_type: int) -> None:
+        self.outs.append(out)
+        self.types.append(kernel_type)
+
+    def _run(self) -> None:
+        c = self.ctx
+        if len(self.outs) == 1:
+            _hip.page_reduce(self.x, self.outs[0], self.loc, c.head_num, c.page_size, self.dim, self.types[0])
+        else:
+            _hip.page_reduce_multi(self.x, self.outs, self.types, self.loc, c.head_num, c.page_size, self.dim)
+
+
+def _record_page_reduce(x, output, loc, ctx: Context, dim: int, reduce_type: ReduceType) -> bool:
+    """Records a page-finish reduction in the current forward_cache scope
+    (joining the newest record when it reduces the same pool for the same
+    loc); False if it must run now.  Only a layout-tagged output is recorded,
+    so reading it through torch runs the record first."""
+    sc = _deferred.current_scope()
+    if sc is None or not _deferred.fusion_enabled() or not isinstance(output, vTensor) or not isinstance(x, vTensor):
+        return False
+    if not _recordable_operands(x, output, loc):
+        return False
+    xp, op, lp = _deferred.plain(x), _deferred.plain(output), _deferred.plain(loc)
+    last = sc.pending[-1] if sc.pending else None
+    if not (isinstance(last, _PendingPageReduce) and last.accepts(xp, op, lp, ctx, dim)):
+        last = _PendingPageReduce(xp, lp, ctx, dim)
+        sc.add(last)
+    last.add(op, _kernel_type(reduce_type))
+    return True
+
+
+def _recordable_operands(x, output, loc) -> bool:
+    """GPU tensors, the output distinct from the pool."""
+    with torch._C.DisableTorchFunctionSubclass():
+        return x.is_cuda and output.is_cuda and loc.is_cuda and output.data_ptr() != x.data_ptr()
 
 
 class Reduce(vOp):
@@ -111,6 +173,9 @@ class Reduce(vOp):
         if output is None:
             assert self.output_buffer is not None, f"{p}internal output buffer is None; did profile() run?"
             output = self.output_buffer
+        if self.impl is reduce_pp and _record_page_reduce(x, output, loc, ctx, self.dim, self.reduce_type):
+            return output
+        _deferred.flush_all()  # recorded reductions first, in program order
         self.impl(x, output, loc, ctx, self.dim, self.reduce_type)
         return output
 
@@ -181,6 +246,7 @@ class MultiReduce(vOp):
 
     def execute(self, x: torch.Tensor, outputs: Sequence[torch.Tensor], loc: torch.Tensor, ctx: Context):
         assert self._ready, f"{self._prefix()}called before profile()"
+        _deferred.flush_all()  # recorded reductions first, in program order
         _hip.page_reduce_multi(x, outputs, [_kernel_type(t) for t in self.reduce_types], loc,
                                ctx.head_num, ctx.page_size, self.dim)
         return list(outputs)

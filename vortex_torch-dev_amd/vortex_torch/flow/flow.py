@@ -28,26 +28,27 @@ from ..abs import ContextBase
 from ..utils import Mode
 
 
-def _ctx_of(args, kwargs):
+def _ctx_of(args, kwargs, pos: int):
     if "ctx" in kwargs:
         return kwargs["ctx"]
-    return args[3] if len(args) > 3 else None
+    return args[pos] if len(args) > pos else None
 
 
-def _scoped_indexer(fn):
-    """Runs a forward_indexer inside a deferral scope when its context is in
-    execute mode (see vortex_torch._deferred): recorded work is fused where
-    possible and everything is finished when the method returns."""
+def _scoped(fn, ctx_pos: int):
+    """Runs a forward_indexer / forward_cache inside a deferral scope when its
+    context is in execute mode (see vortex_torch._deferred): recorded work is
+    fused where possible and everything is finished when the method returns.
+    ctx_pos: position of ctx among the method's arguments after self."""
 
     @functools.wraps(fn)
-    def forward_indexer(self, *args, **kwargs):
-        ctx = _ctx_of(args, kwargs)
+    def scoped(self, *args, **kwargs):
+        ctx = _ctx_of(args, kwargs, ctx_pos)
         mode = getattr(ctx, "mode", None)
         with _deferred.scope(active=mode is None or mode == Mode.execute):
             return fn(self, *args, **kwargs)
 
-    forward_indexer._vtx_scoped = True
-    return forward_indexer
+    scoped._vtx_scoped = True
+    return scoped
 
 
 class vFlow(ABC):
@@ -56,9 +57,10 @@ class vFlow(ABC):
 
     def __init_subclass__(cls, **kwargs):
         super().__init_subclass__(**kwargs)
-        fn = cls.__dict__.get("forward_indexer")
-        if fn is not None and not getattr(fn, "_vtx_scoped", False) and callable(fn):
-            cls.forward_indexer = _scoped_indexer(fn)
+        for name, ctx_pos in (("forward_indexer", 3), ("forward_cache", 2)):
+            fn = cls.__dict__.get(name)
+            if fn is not None and not getattr(fn, "_vtx_scoped", False) and callable(fn):
+                setattr(cls, name, _scoped(fn, ctx_pos))
 
     @abstractmethod
     def forward_indexer(self, q: torch.Tensor, o: torch.Tensor, cache: Dict[str, torch.Tensor],
