@@ -393,9 +393,9 @@ def bench_flow(args, dev) -> dict:
     seg_n = np.diff(plan["dense_indptr"].astype(np.int64)) - batch.bos - batch.eos
     sel = int((seg_n > batch.topk).sum()) * batch.topk * 4
     # per covered page: its row(s) (envelopes max + min, or one centroid), its
-    # page id, and the score outputs (per-head scores + page score, or the page score)
+    # page id, and the fused kernel's outputs (per-head scores + page score)
     rows_per_page = 2 if args.flow == "quest" else 1
-    outs = 2 * G + 2 if args.flow == "gqa" else 2
+    outs = 2 * G + 2
     per_layer = B * H * G * D * 2 + covered * (rows_per_page * 2 * D + 4 + outs) + sel
     gbps = per_layer * args.layers / (us_step * 1e-6) / 1e9
     print(f"[bench] {name} step {us_step:.1f} us", file=sys.stderr, flush=True)
