@@ -59,8 +59,9 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per fused-indexer launch from the FETCH_SIZE and WRITE_SIZE
 # counter passes over --traffic-probe (each scaled by what the counter reads
 # for the probe's copy kernel of known size); the per-launch traffic does not
-# depend on the layer count (34,072 KiB read + 464 KiB written at C2).
-TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_364_864}
+# depend on the layer count (34,216 KiB read + 466 KiB written at C2, the
+# launch including the layer's CMean).
+TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_514_368}
 
 
 def _parse():
@@ -112,7 +113,11 @@ def fused_kernel_name(batch: W.DecodeBatch) -> str:
         return f"indexer_split_kernel<256, {lpr}, {vpl}, {small_pass * (2 if large else 1)}>"
     mp = batch.max_pages_per_request
     T = 256 if mp <= 256 else (512 if mp <= 1024 else 1024)
-    return f"indexer_fused_kernel<{T}, {lpr}, {vpl}>"
+    # the decode CMean (loc: one token per request) runs in the same launch
+    # for rows of one vector per lane, with loc in one register per lane up
+    # to 64 tokens, four up to 256
+    cm = (1 if batch.batch <= 64 else 4) if vpl == 1 and batch.batch <= 256 else 0
+    return f"indexer_fused_kernel<{T}, {lpr}, {vpl}, {cm}>"
 
 
 class DecodeStep:
@@ -171,12 +176,14 @@ class DecodeStep:
             f.forward_indexer(q, self.o, cache, self.ictx)
 
     def indexer_kernels_only(self):
-        """The fused indexer kernel of every layer, launched directly."""
+        """The fused indexer kernel of every layer, launched directly as the
+        step launches it: with the layer's decode CMean (the mean that
+        forward_cache leaves for forward_indexer) in the same launch."""
         from vortex_torch import _hip
         from vortex_torch._deferred import fused_layout
 
         ic, b = self.ictx, self.batch
-        for i, (f, (_, cen, qp)) in enumerate(zip(self.flows, self.plain)):
+        for i, (f, (k, cen, qp)) in enumerate(zip(self.flows, self.plain)):
             with torch._C.DisableTorchFunctionSubclass():
                 if self.premeaned is not None:  # G > 2: the step hands the kernel torch's mean
                     q, x_out = self.premeaned[i], None
@@ -186,7 +193,7 @@ class DecodeStep:
                                    ic.sparse_kv_indptr, ic.dense_kv_indices, ic.sparse_kv_indices,
                                    b.batch * b.num_kv_heads, b.topk, b.bos, b.eos,
                                    b.max_pages_per_request, seg_counters=f.output_func.seg_counters,
-                                   mode=fused_layout())
+                                   mode=fused_layout(), cmean=(k, self.loc, b.num_kv_heads))
 
 
 def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: np.ndarray) -> dict:
@@ -206,11 +213,14 @@ def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: n
     # fused kernel: query in (the G heads, or torch's mean when G > 2), mean out
     # (G <= 2), row ids + centroid rows in, scores out, ids out
     fused_q = q_in + q_out if G <= 2 else q_out
-    fused = fused_q + covered * (4 + 2 * D + 2) + sel_segs * batch.topk * 4 + (B * H + 1) * 8
     ndense = int(dip[-1])
     plan_b = ndense * 4 + (ndense // H) * 4 + 2 * (B * H + 1) * 4 + int(plan["sparse_indptr"][-1]) * 4 + B * 16
     finishing = int(((loc_host + 1) % P == 0).sum()) * H
-    cmean = finishing * (P * 2 * D + 2 * D) + B * 8
+    # CMean: the K tiles of the pages the step's tokens close, their centroids
+    # out, and loc
+    cmean = finishing * (P * 2 * D + 2 * D) + loc_host.size * 8
+    # the fused launch also runs the layer's CMean
+    fused = fused_q + covered * (4 + 2 * D + 2) + sel_segs * batch.topk * 4 + (B * H + 1) * 8 + cmean
     per_layer = gemv + topk + qmean + cmean
     return {"gemv": gemv, "topk": topk, "qmean": qmean, "cmean": cmean, "plan": plan_b, "fused": fused,
             "step": plan_b + layers * per_layer, "covered_pages": covered}
@@ -359,7 +369,7 @@ def bench_decode(args, dev) -> dict:
         "algorithmic_bytes_per_step": nbytes["step"],
         "unfused_us_per_step": unfused,
         "roofline": {
-            "kernel": f"{kernel} (q-mean + GeMV + top-k, one layer)",
+            "kernel": f"{kernel} (CMean of the closed pages + q-mean + GeMV + top-k, one layer)",
             "bound": "hbm",
             "achieved": round(fused_gbps, 1),
             "peak": HBM_PEAK_GBPS,

@@ -205,6 +205,32 @@ int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
 int vtx_indexer_fused_supported(int32_t head_dim);
 
 /*
+ * vtx_indexer_fused preceded by the layer's page-finish mean into y: the
+ * results of vtx_page_reduce(k_cache, k_rows, page_size, head_dim, y, BF16,
+ * y_rows, loc, nnz, num_kv_heads, page_size, 1, VTX_REDUCE_MEAN) followed by
+ * vtx_indexer_fused with the same arguments, bit for bit (y is written).  No
+ * single counterpart in the reference: it is CMean
+ * (cache/triton_kernels/reduce_impl.py:7-89, the cache step of
+ * block_sparse_attention, vortex_torch/flow/algorithms.py:20-235) and the
+ * layer's indexer step in one launch.  For head_dim 64 / 128, nnz <= 256 and
+ * the one-workgroup-per-segment layout the mean runs in extra workgroups of
+ * the same launch, and a scored page whose centroid it rewrites is scored
+ * against the fresh centroid; otherwise it is its own launch, first.
+ * k_cache: bf16 [k_rows, page_size, head_dim] with row = page * H + h.
+ */
+int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                            const uint16_t* x, uint16_t* x_out, uint16_t* y, int64_t y_rows,
+                            uint16_t* score, int64_t score_len,
+                            const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                            const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                            int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                            int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                            int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
+                            int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
+                            const uint16_t* k_cache, int64_t k_rows, int32_t page_size,
+                            int32_t num_kv_heads, const int64_t* loc, int64_t nnz, void* stream);
+
+/*
  * Fused indexer step of the GQA flow: GeMM of the group_size query heads
  * with every middle page's centroid, optional segment softmax per query
  * head, maximum over the query heads, top-k select — one launch, one

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import workloads as W
-from vortex_torch import _hip
+from vortex_torch import _deferred, _hip
 from vortex_torch.abs import FORMAT, as_vtensor
 from vortex_torch.flow import algorithms, build_vflow, registry
 from vortex_torch.cache import reduce as CR
@@ -30,7 +30,8 @@ def launches(monkeypatch):
     monkeypatch.setattr(_hip, "topk_select", rec("topk"))
     monkeypatch.setattr(_hip, "page_reduce", rec("page_reduce"))
     monkeypatch.setattr(_hip, "page_reduce_multi", lambda x, outs, *a, **k: log.append(f"page_reduce_multi{len(outs)}"))
-    return log
+    yield log
+    _deferred._tls.carry = None
 
 
 def _run(flow_name, cache_step=False, indexer=True):
@@ -120,4 +121,114 @@ def test_quest_cache_reductions_unfused(launches, monkeypatch):
 
 def test_single_cache_reduction_stays_single(launches):
     _run("gqa_block_sparse_attention", cache_step=True, indexer=False)
+    assert launches == []  # carried for the next forward_indexer
+    _deferred.flush_carry()
     assert launches == ["page_reduce"]
+
+
+
+# ------------------------------------------------ the carried page-finish mean
+@pytest.fixture
+def carry_launches(monkeypatch):
+    """Kernel wrappers replaced by recorders that, like the real ones, first
+    run the deferral layer's pre-launch hook."""
+    from vortex_torch.indexer import matmul as MM
+
+    log = []
+
+    def rec(name):
+        def f(*a, **k):
+            _hip._pre_launch()
+            log.append(name + ("+cmean" if k.get("cmean") is not None else ""))
+        return f
+
+    monkeypatch.setattr(CR, "_recordable_operands", lambda x, out, loc: True)
+    monkeypatch.setattr(MM, "_fusable", lambda x, y, ctx: True)
+    for name in ("page_reduce", "page_reduce_multi", "indexer_fused", "gemv_paged", "topk_select"):
+        monkeypatch.setattr(_hip, name, rec(name))
+    yield log
+    _deferred._tls.carry = None
+
+
+class _Layer:
+    """block_sparse_attention on C1-shaped CPU tensors, execute mode."""
+
+    def __init__(self, flow_name="block_sparse_attention"):
+        batch = W.c1()
+        self.ic, self.cc = W.make_contexts(batch, "cpu")
+        self.flow = build_vflow(flow_name)
+        H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+        rows = batch.pool_pages * H
+        self.cache = {"k": as_vtensor(torch.zeros((rows, P, D), dtype=torch.bfloat16), FORMAT.PAGED)}
+        for name, (r, c) in self.flow.create_cache(P, D).items():
+            self.cache[name] = as_vtensor(torch.zeros((rows, r, c), dtype=torch.bfloat16), FORMAT.PAGED)
+        self.q = as_vtensor(torch.zeros((batch.batch * H, G, D), dtype=torch.bfloat16), FORMAT.BATCHED)
+        self.o = as_vtensor(self.ic.sparse_kv_indices.view(-1, 1, 1), FORMAT.RAGGED)
+        self.loc = torch.arange(batch.batch, dtype=torch.int64) * P + P - 1
+        self.ic.profile()
+        self.cc.profile()
+        self.flow.forward_cache(self.cache, self.loc, self.cc)
+        self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
+        self.ic.execute()
+        self.cc.execute()
+
+    def cache_step(self):
+        self.flow.forward_cache(self.cache, self.loc, self.cc)
+
+    def indexer_step(self):
+        self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
+
+
+def test_cmean_runs_inside_the_next_indexer_launch(carry_launches):
+    layer = _Layer()
+    layer.cache_step()
+    assert carry_launches == []  # carried
+    layer.indexer_step()
+    assert carry_launches == ["indexer_fused+cmean"]
+
+
+def test_carried_cmean_runs_before_a_torch_read(carry_launches):
+    layer = _Layer()
+    layer.cache_step()
+    float(layer.cache["centroids"].sum())
+    assert carry_launches == ["page_reduce"]
+    layer.indexer_step()
+    assert carry_launches == ["page_reduce", "indexer_fused"]
+
+
+def test_carried_cmean_runs_before_the_next_cache_step(carry_launches):
+    a, b = _Layer(), _Layer()
+    a.cache_step()
+    b.cache_step()
+    assert carry_launches == ["page_reduce"]  # a's, at b's forward_cache
+    b.indexer_step()
+    assert carry_launches == ["page_reduce", "indexer_fused+cmean"]
+
+
+def test_carried_cmean_runs_before_any_other_launch(carry_launches, monkeypatch):
+    layer = _Layer()
+    layer.cache_step()
+    _hip.topk_select(None)  # any other kernel of the package
+    assert carry_launches == ["page_reduce", "topk_select"]
+
+
+def test_carried_cmean_for_other_centroids_is_not_consumed(carry_launches):
+    a, b = _Layer(), _Layer()
+    a.cache_step()
+    b.indexer_step()  # scores b's centroids: a's mean runs first, on its own
+    assert carry_launches == ["page_reduce", "indexer_fused"]
+
+
+def test_unconsumed_carry_runs_at_indexer_exit(carry_launches):
+    layer = _Layer("gqa_quest_sparse_attention")  # CMax + CMin: one multi pass, not carried
+    layer.cache_step()
+    assert carry_launches == ["page_reduce_multi"]
+
+
+def test_carry_off(carry_launches, monkeypatch):
+    monkeypatch.setenv("VORTEX_FUSE_CMEAN", "0")
+    layer = _Layer()
+    layer.cache_step()
+    assert carry_launches == ["page_reduce"]
+    layer.indexer_step()
+    assert carry_launches == ["page_reduce", "indexer_fused"]

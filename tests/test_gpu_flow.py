@@ -167,9 +167,9 @@ class _FlowRun:
         self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "eos0"])
 def test_flow_fused_equals_unfused(gpu, name, monkeypatch):
-    batch = getattr(W, name)()
+    batch = _cmean_case(name)[0] if name == "eos0" else getattr(W, name)()
     results = {}
     for fuse in ("1", "0"):
         monkeypatch.setenv("VORTEX_FUSE", fuse)
@@ -263,3 +263,106 @@ def test_deferred_mean_materializes_on_use(gpu):
         expect = q.as_subclass(torch.Tensor).mean(dim=1, keepdim=True)
         assert torch.equal(m.as_subclass(torch.Tensor), expect)
         assert torch.equal(doubled.as_subclass(torch.Tensor), expect * 2)
+
+
+# ------------------------------------------- CMean inside the fused launch
+def _cmean_case(name):
+    """(batch, loc) for the fused CMean + indexer launch."""
+    if name == "eos0":  # every request's last page closes and is a middle page (eos 0)
+        b = W.make_batch([1024, 2048, 640, 4096, 512], pool_pages=900, seed=21, eos=0, topk=12)
+        return b, W.decode_loc(b)
+    if name == "mid":  # closing slots of middle pages, several per request
+        b = W.make_batch([3000, 5000, 1800], pool_pages=700, seed=22, topk=20)
+        g = torch.Generator().manual_seed(5)
+        slots = []
+        for pages in b.pages:
+            pick = torch.randperm(len(pages) - 2, generator=g)[:9] + 1
+            slots += [int(pages[i]) * b.page_size + b.page_size - 1 for i in pick]
+        slots += [7, 16 * 3 + 2]  # tokens that close nothing
+        return b, torch.as_tensor(slots, dtype=torch.int64)
+    if name == "d64":
+        b = W.make_batch([3000, 1500, 700], pool_pages=400, seed=23, head_dim=64, group_size=1, eos=0)
+        return b, W.decode_loc(b)
+    if name == "big_loc":  # more loc entries than one launch scans: CMean launched first
+        b = W.make_batch([4096, 4096], pool_pages=600, seed=24)
+        return b, torch.arange(300, dtype=torch.int64) * 3
+    if name == "d256":  # wider rows: CMean launched first
+        b = W.make_batch([2000, 3000], pool_pages=400, seed=25, head_dim=256, eos=0)
+        return b, W.decode_loc(b)
+    if name.startswith("r"):
+        b = W.random_small(int(name[1:]))
+        return b, W.decode_loc(b)
+    b = getattr(W, name)()
+    return b, W.decode_loc(b)
+
+
+@pytest.mark.parametrize("mode", [_hip.FUSED_AUTO, _hip.FUSED_SPLIT])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "eos0", "mid", "d64", "big_loc", "d256", "r3", "r6", "r9"])
+def test_fused_cmean_equals_separate_launches(gpu, name, mode):
+    """vtx_indexer_fused_cmean writes what vtx_page_reduce then
+    vtx_indexer_fused write: centroids, q-mean, scores and block table."""
+    dev = gpu
+    batch, loc = _cmean_case(name)
+    loc = loc.to(dev)
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+    S = batch.batch * H
+    rows = batch.pool_pages * H
+    q = W.randn_bf16((S, G, D), 1, dev)
+    k = W.randn_bf16((rows, P, D), 3, dev)
+    y0 = W.randn_bf16((rows, 1, D), 2, dev, std=0.25)
+    n_dense = ic.dense_kv_indices.numel()
+    out = {}
+    for fused in (False, True):
+        y = y0.clone()
+        qm = torch.zeros((S, 1, D), device=dev, dtype=torch.bfloat16)
+        sc = torch.full((n_dense, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
+        sp = ic.sparse_kv_indices.clone()
+        counters = torch.zeros(S, dtype=torch.int32, device=dev)
+        x_out = qm if G <= 2 else None
+        qin = q if G <= 2 else q.mean(dim=1, keepdim=True)
+        args = (qin, x_out, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp, S,
+                batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+        if fused:
+            _hip.indexer_fused(*args, seg_counters=counters, mode=mode, cmean=(k, loc, H))
+        else:
+            _hip.page_reduce(k, y, loc, H, P, 1, _hip.REDUCE_MEAN)
+            _hip.indexer_fused(*args, seg_counters=counters, mode=mode)
+        torch.cuda.synchronize()
+        out[fused] = (_bits(y), _bits(qm), _bits(sc), _np(sp))
+    assert (out[True][0] != _bits(y0)).any() or int(((loc + 1) % P == 0).sum()) == 0
+    for a, b in zip(out[False], out[True]):
+        np.testing.assert_array_equal(a, b)
+
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "eos0", "r3", "r9"])
+def test_flow_cmean_carried_into_indexer_launch(gpu, name, monkeypatch):
+    """forward_cache's CMean runs inside the next forward_indexer's fused
+    launch (VORTEX_FUSE_CMEAN=1) with the same centroids, scores and block
+    table as when it is launched on its own (=0)."""
+    batch = _cmean_case(name)[0]
+    seen = []
+    real = _hip.indexer_fused
+    monkeypatch.setattr(_hip, "indexer_fused", lambda *a, **k: (seen.append(k.get("cmean") is not None),
+                                                                 real(*a, **k)))
+    results = {}
+    for carry in ("1", "0"):
+        monkeypatch.setenv("VORTEX_FUSE_CMEAN", carry)
+        run = _FlowRun(batch, gpu)
+        seen.clear()
+        run.step()
+        torch.cuda.synchronize()
+        with torch._C.DisableTorchFunctionSubclass():
+            results[carry] = (_bits(run.cen), _np(run.ic.sparse_kv_indices), _bits(run.flow.gemv.output_buffer))
+        assert seen == ([carry == "1"] if seen else [])
+    np.testing.assert_array_equal(results["1"][0], results["0"][0])
+    np.testing.assert_array_equal(results["1"][1], results["0"][1])
+    # scores: the positions the GeMV covers (the planner's workloads)
+    ref = O.plan_decode(_np(batch.seq_lens), _np(batch.req_to_token), _np(batch.req_indices), batch.page_size,
+                        batch.num_kv_heads, batch.topk, batch.bos, batch.eos, batch.max_chunk)
+    cov = np.zeros(results["1"][2].size, dtype=bool)
+    for off, ln in zip(ref["winfo_off"], ref["winfo_len"]):
+        cov[off:off + ln] = True
+    np.testing.assert_array_equal(results["1"][2][cov], results["0"][2][cov])

@@ -18,6 +18,15 @@
 // select -> stores.  The scores never leave the chip for the select and,
 // for segments that fit the LDS row cache, neither do the winners' page ids.
 //
+// The layer's decode CMean (vtx_indexer_fused_cmean): the page-finish mean
+// of the pages the step's tokens close runs in the same launch.  Every wave
+// reads loc first (at most 256 entries, held in registers: no LDS, no
+// barrier) and after its passes reduces its share of the closed tiles with
+// the page-reduce kernel's own code (vtx_page_reduce.h); a scored page whose
+// centroid this CMean rewrites (a closed page that is a middle page: eos = 0,
+// or loc entries of earlier pages) is scored after the loop against the
+// centroid recomputed from its K tile, the bits the separate launches give.
+//
 // Row scoring: a segment's middle pages are split evenly over the waves, at
 // most kPass pages per wave pass (64 for rows of one 16-byte vector per lane,
 // 32 for wider rows), LPR lanes x VPL 16-byte vectors per row.  The per-lane
@@ -26,10 +35,13 @@
 // kernel's for the same query.
 #include "vtx_device.h"
 #include "vtx_host.h"
+#include "vtx_page_reduce.h"
 #include "vtx_score.h"
 #include "vtx_select.h"
 
 namespace {
+
+constexpr int kCmLoc = 256;  // loc entries a launch with an in-kernel CMean scans
 
 struct FusedArgs {
   const uint16_t* q;  // [S, G, D] when G > 0
@@ -53,6 +65,140 @@ struct FusedArgs {
   int32_t row_cap;   // segments up to this many middle pages are held in LDS
   int32_t segments;  // eff_batch_size; the grid covers all q_rows
 };
+
+// The layer's decode CMean run inside a fused launch (kCm): the mean over
+// each closed page's [rows_per_tile, cols] K tile into y (`out`), whose
+// rows are the centroids the launch scores — a scored page that this CMean
+// closes is scored against its fresh centroid (fresh_score).
+struct CmArgs {
+  const uint16_t* x;  // K pool [x_rows, rows_per_tile, cols]
+  int64_t x_rows;
+  int32_t rows_per_tile, cols;
+  uint16_t* out;      // == y
+  int64_t out_rows;
+  const int64_t* loc;
+  int64_t nnz;
+  int32_t heads, page;
+};
+
+// The pages this launch's CMean closes, as one wave holds them (no LDS, no
+// barrier): lane l keeps, for loc entries j * 64 + l (j < kLocRegs), the
+// first tile row (page * H) of the page the entry closes, or -1; mask[j] is
+// the ballot of the closing entries, so "the i-th closed page" is the i-th
+// set bit in loc order, the order the page-reduce kernel lists them in.
+template <int kLocRegs>
+struct Closing {
+  int base[kLocRegs];
+  uint64_t mask[kLocRegs];
+  int count;
+};
+
+template <int kLocRegs>
+__device__ __forceinline__ void closing_load(const CmArgs& cm, long long (&pos)[kLocRegs]) {
+  const int lane = vtx::lane_id();
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    const long long e = (long long)j * vtx::kWave + lane;
+    pos[j] = e < cm.nnz ? cm.loc[e] : 0;
+  }
+}
+
+template <int kLocRegs>
+__device__ __forceinline__ Closing<kLocRegs> closing_build(const CmArgs& cm, const long long (&pos)[kLocRegs]) {
+  const int lane = vtx::lane_id();
+  Closing<kLocRegs> c;
+  c.count = 0;
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    const long long e = (long long)j * vtx::kWave + lane;
+    const bool closes = e < cm.nnz && (pos[j] + 1) % cm.page == 0;  // C semantics, as page-reduce
+    c.base[j] = closes ? (int)((pos[j] / cm.page) * cm.heads) : -1;
+    c.mask[j] = __ballot(closes);
+    c.count += __popcll(c.mask[j]);
+  }
+  return c;
+}
+
+// First tile row of the i-th closed page (i < c.count); wave-uniform i.
+template <int kLocRegs>
+__device__ __forceinline__ int closing_base(const Closing<kLocRegs>& c, int i) {
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    const int n = __popcll(c.mask[j]);
+    if (i < n) {
+      uint64_t m = c.mask[j];
+      for (int k = 0; k < i; ++k) m &= m - 1;
+      return __builtin_amdgcn_readlane(c.base[j], __ffsll((long long)m) - 1);
+    }
+    i -= n;
+  }
+  return -1;
+}
+
+// Tiles first, first + stride, ... of the closed pages (tile t: head t % H
+// of closed page t / H): the mean over each tile's rows into cm.out, exactly
+// as reduce_rows_vec_kernel<LPR, kNeedSum> computes it.  Wave-level.
+template <int LPR, int kLocRegs>
+__device__ __forceinline__ void cmean_tiles(const CmArgs& cm, const Closing<kLocRegs>& c, int first, int stride,
+                                            int grp, int cv) {
+  const int tiles = c.count * cm.heads;
+  for (int t = first; t < tiles; t += stride) {
+    const long long row = (long long)closing_base(c, t / cm.heads) + (t % cm.heads);
+    if (!vtx::tile_in_range(cm, row)) continue;
+    vtx::Acc acc[8];
+    vtx::tile_stats_vec<LPR, vtx::kNeedSum>(cm.x, row, cm.rows_per_tile, cm.cols, grp, cv, acc);
+    if (grp == 0) {
+      uint32_t bb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bb[e] = vtx::acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
+      vtx::st16(cm.out + row * cm.cols + cv * 8, vtx::U4{bb[0] | (bb[1] << 16), bb[2] | (bb[3] << 16),
+                                                        bb[4] | (bb[5] << 16), bb[6] | (bb[7] << 16)});
+    }
+  }
+}
+
+// Score of tile row `rid` against the freshly reduced centroid, for a page
+// the in-kernel CMean closes (the row in y may not be written yet): the
+// wave recomputes the centroid from the page's K tile with the CMean's own
+// arithmetic and scores it with the lane's dot_row chain and the xor tree
+// over the LPR lanes — the bits score_pass gives for that centroid row.
+// All 64 lanes take part and all return the score.  Rows of one 16-byte
+// vector per lane (VPL == 1).
+template <int LPR>
+__device__ __forceinline__ float fresh_score(const CmArgs& cm, int rid, const float (&xs)[1][8],
+                                             int grp, int col) {
+  vtx::Acc acc[8];
+  vtx::tile_stats_vec<LPR, vtx::kNeedSum>(cm.x, rid, cm.rows_per_tile, cm.cols, grp, col, acc);
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = vtx::acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
+  const vtx::U4 cen[1] = {vtx::U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
+                                  b[6] | (b[7] << 16)}};
+  float f = vtx::dot_row<1>(cen, xs);
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) f += __shfl_xor(f, d, vtx::kWave);
+  return f;
+}
+
+// Whether the lane's pass position (r >= 0, row my_rid) is a tile the
+// in-kernel CMean writes: a row in [page * H, page * H + H) of a closed page,
+// inside the pool and the centroid pool.
+template <int kLocRegs>
+__device__ __forceinline__ bool closes_here(const CmArgs& cm, const Closing<kLocRegs>& c, int r, int my_rid) {
+  const bool cand = r >= 0 && my_rid >= 0 && my_rid < cm.x_rows && my_rid < cm.out_rows;
+  bool fix = false;
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    uint64_t m = c.mask[j];
+    while (m) {  // wave-uniform
+      const int l = __ffsll((long long)m) - 1;
+      m &= m - 1;
+      const int base = __builtin_amdgcn_readlane(c.base[j], l);
+      fix |= (unsigned)(my_rid - base) < (unsigned)cm.heads;
+    }
+  }
+  return cand && fix;
+}
 
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
 // fp32 mean of its G rows (torch's mean), or the row itself when G == 0.
@@ -122,8 +268,8 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
 }
 
 // One workgroup per segment: scores into LDS, select in LDS.
-template <int T, int LPR, int VPL>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a) {
+template <int T, int LPR, int VPL, int kCmRegs>
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a, CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   constexpr int kPass = vtx::segment_pass<VPL>();
@@ -140,6 +286,16 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int k = a.topk;
   const int D = a.dim;
   const bool store_mean = wave == 0 && grp == 0;
+  __shared__ int32_t fix_pos[kCmLoc];  // middle positions scored in step 4b
+  __shared__ int fix_n;
+  // kCmRegs > 0: this launch runs the layer's CMean over up to 64 * kCmRegs loc entries
+  constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
+  constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
+
+  // ---- 0. with the in-kernel CMean, loc (issued first, so that waiting for
+  // it waits for nothing else; used once the first row ids are requested)
+  long long cm_pos[kLocRegs];
+  if constexpr (cm_on) closing_load(cma, cm_pos);
 
   // ---- 1. query rows (issued first: only needed once centroid rows arrive)
   vtx::U4 qv[kQRegs][VPL];
@@ -161,6 +317,9 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     n = (long long)a.dindptr[seg + 1] - a.eos - start;
     obase = (long long)a.sindptr[seg] + a.bos;
   }
+  // pages the in-kernel CMean closes (its loc load overlaps the bounds')
+  Closing<kLocRegs> closing{};
+  int n_close = 0;
   bool active = is_seg && k > 0 && n > k;
   if (active && (start < 0 || start + n > a.score_len || start + n > a.didx_len || obase < 0 ||
                  obase + k > a.sidx_len))
@@ -175,42 +334,91 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   float xs[VPL][8];
   if (!active) {  // uniform over the workgroup
     if (a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-    return;
+    if constexpr (!cm_on) return;  // (with the CMean: its tiles first, below)
   }
-  vtx::select_init<T>(sel, k, sh);
-  __syncthreads();  // histogram cleared before any wave counts into it
-  bool have_mean = false;
-
-  // ---- 4. scores: the pages are split evenly over the waves (one pass
-  // each up to kWaves * kPass pages, so no wave waits on a second round
-  // trip while others idle); row ids come straight from global memory
   const int32_t* dseg = a.didx + start;
-  long long share = (n + kWaves - 1) / kWaves;
-  share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
-  if (share > kPass) share = kPass;
-  for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
-    const int cnt = (int)min(share, n - p0);
-    // one coalesced load of the pass's row ids (lane l holds position l)
-    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
-    if (!have_mean) {
-      query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-      have_mean = true;
+  long long share = 0;
+  bool have_mean = false;
+  if (active) {  // uniform
+    vtx::select_init<T>(sel, k, sh);
+    if (cm_on && tid == 0) fix_n = 0;
+    __syncthreads();  // histogram cleared before any wave counts into it
+    if constexpr (cm_on) {
+      closing = closing_build(cma, cm_pos);
+      n_close = closing.count;
     }
-    int r;
-    const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
-    const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
-    if (r >= 0) {
-      const uint32_t sb = vtx::f32_to_bf16(sc);
-      const uint32_t key = vtx::score_key(sb);
-      a.score[start + p0 + r] = (uint16_t)sb;
-      if (cached) {
-        keys[p0 + r] = (uint16_t)key;
-        rows[p0 + r] = my_rid;
+
+    // ---- 4. scores: the pages are split evenly over the waves (one pass
+    // each up to kWaves * kPass pages, so no wave waits on a second round
+    // trip while others idle); row ids come straight from global memory
+    share = (n + kWaves - 1) / kWaves;
+    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+    if (share > kPass) share = kPass;
+    for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
+      const int cnt = (int)min(share, n - p0);
+      // one coalesced load of the pass's row ids (lane l holds position l)
+      const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
+      if (!have_mean) {
+        query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+        have_mean = true;
       }
-      vtx::select_count<T>(key, sh);
+      int r;
+      const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+      const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
+      if (cm_on && n_close > 0 && closes_here(cma, closing, r, my_rid)) {
+        // the in-kernel CMean rewrites this page's centroid: scored after the loop
+        fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);
+        r = -1;
+      }
+      if (r >= 0) {
+        const uint32_t sb = vtx::f32_to_bf16(sc);
+        const uint32_t key = vtx::score_key(sb);
+        a.score[start + p0 + r] = (uint16_t)sb;
+        if (cached) {
+          keys[p0 + r] = (uint16_t)key;
+          rows[p0 + r] = my_rid;
+        }
+        vtx::select_count<T>(key, sh);
+      }
     }
+  }
+  // This launch's CMean: wave w of workgroup b reduces tiles w * grid + b,
+  // + waves * grid, ... (one tile per wave 0 for up to `grid` tiles), after
+  // its passes (the registers of the scoring loop are free by then).
+  if constexpr (cm_on) {
+    if (!active) {  // the closed pages
+      closing = closing_build(cma, cm_pos);
+      n_close = closing.count;
+    }
+    cmean_tiles<LPR, kLocRegs>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
+                               col);
+    if (!active) return;
   }
   __syncthreads();
+
+  // ---- 4b. pages whose centroid this launch's CMean rewrites (at most one
+  // per closed page): a wave each, against the fresh centroid
+  if constexpr (cm_on) {
+    if (n_close > 0 && fix_n > 0) {  // uniform
+      if (!have_mean) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+      for (int i = wave; i < fix_n; i += kWaves) {
+        const int pos = fix_pos[i];
+        const int rid = dseg[pos];
+        const float f = fresh_score<LPR>(cma, rid, xs, grp, col);
+        if (lane == 0) {
+          const uint32_t sb = vtx::f32_to_bf16(f);
+          const uint32_t key = vtx::score_key(sb);
+          a.score[start + pos] = (uint16_t)sb;
+          if (cached) {
+            keys[pos] = (uint16_t)key;
+            rows[pos] = rid;
+          }
+          vtx::select_count<T>(key, sh);
+        }
+      }
+      __syncthreads();
+    }
+  }
 
   // ---- 5. top-k of the segment
   if (cached) {
@@ -377,13 +585,29 @@ constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS; the select tables take up
 constexpr int kMaxTopk = 4096;
 
 template <int T>
-int launch_dim(const FusedArgs& a, int blocks, size_t lds, hipStream_t s) {
+int launch_dim(const FusedArgs& a, const CmArgs* cm, int blocks, size_t lds, hipStream_t s) {
+  const CmArgs none{};
+  if (cm) {  // the in-kernel CMean: rows of one 16-byte vector per lane
+    const bool one = cm->nnz <= vtx::kWave;  // loc in one register per lane
+    switch (a.dim) {
+      case 64:
+        if (one) indexer_fused_kernel<T, 8, 1, 1><<<blocks, T, lds, s>>>(a, *cm);
+        else indexer_fused_kernel<T, 8, 1, kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
+        break;
+      case 128:
+        if (one) indexer_fused_kernel<T, 16, 1, 1><<<blocks, T, lds, s>>>(a, *cm);
+        else indexer_fused_kernel<T, 16, 1, kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
+        break;
+      default: return vtx::fail(VTX_E_INVALID, "indexer_fused: in-kernel CMean needs head_dim 64 or 128");
+    }
+    return vtx::check_launch("indexer_fused (with CMean)");
+  }
   switch (a.dim) {
-    case 64: indexer_fused_kernel<T, 8, 1><<<blocks, T, lds, s>>>(a); break;
-    case 128: indexer_fused_kernel<T, 16, 1><<<blocks, T, lds, s>>>(a); break;
-    case 256: indexer_fused_kernel<T, 16, 2><<<blocks, T, lds, s>>>(a); break;
-    case 512: indexer_fused_kernel<T, 16, 4><<<blocks, T, lds, s>>>(a); break;
-    case 576: indexer_fused_kernel<T, 8, 9><<<blocks, T, lds, s>>>(a); break;
+    case 64: indexer_fused_kernel<T, 8, 1, 0><<<blocks, T, lds, s>>>(a, none); break;
+    case 128: indexer_fused_kernel<T, 16, 1, 0><<<blocks, T, lds, s>>>(a, none); break;
+    case 256: indexer_fused_kernel<T, 16, 2, 0><<<blocks, T, lds, s>>>(a, none); break;
+    case 512: indexer_fused_kernel<T, 16, 4, 0><<<blocks, T, lds, s>>>(a, none); break;
+    case 576: indexer_fused_kernel<T, 8, 9, 0><<<blocks, T, lds, s>>>(a, none); break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_fused");
@@ -422,6 +646,27 @@ extern "C" int vtx_indexer_fused_supported(int32_t head_dim) {
   return head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512 || head_dim == 576;
 }
 
+namespace {
+
+// The decode CMean a fused launch may run first (vtx_indexer_fused_cmean).
+struct CmeanSpec {
+  const uint16_t* k;
+  int64_t k_rows;
+  int32_t page_size, heads;
+  const int64_t* loc;
+  int64_t nnz;
+};
+
+int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* x, uint16_t* x_out,
+               const uint16_t* y, int64_t y_rows, uint16_t* score, int64_t score_len,
+               const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+               int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+               int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
+               int32_t max_num_pages, int32_t head_dim, int32_t* seg_counters, int64_t seg_counters_len,
+               int32_t mode, const CmeanSpec* cms, void* stream);
+
+}  // namespace
+
 extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                                  const uint16_t* x, uint16_t* x_out, const uint16_t* y,
                                  int64_t y_rows, uint16_t* score, int64_t score_len,
@@ -433,6 +678,43 @@ extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t grou
                                  int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
                                  void* stream) {
   vtx::clear_error();
+  return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
+                    sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
+                    sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
+                    head_dim, seg_counters, seg_counters_len, mode, nullptr, stream);
+}
+
+extern "C" int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                                       const uint16_t* x, uint16_t* x_out, uint16_t* y, int64_t y_rows,
+                                       uint16_t* score, int64_t score_len, const int32_t* dense_kv_indptr,
+                                       const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+                                       int64_t dense_kv_indices_len, int32_t* sparse_kv_indices,
+                                       int64_t sparse_kv_indices_len, int32_t eff_batch_size, int32_t topk_val,
+                                       int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
+                                       int32_t head_dim, int32_t* seg_counters, int64_t seg_counters_len,
+                                       int32_t mode, const uint16_t* k_cache, int64_t k_rows,
+                                       int32_t page_size, int32_t num_kv_heads, const int64_t* loc, int64_t nnz,
+                                       void* stream) {
+  vtx::clear_error();
+  if (!k_cache || (nnz > 0 && !loc)) return vtx::fail(VTX_E_INVALID, "indexer_fused_cmean: null K pool or loc");
+  if (page_size < 1 || num_kv_heads < 1 || k_rows < 0 || nnz < 0)
+    return vtx::fail(VTX_E_INVALID, "indexer_fused_cmean: bad CMean sizes");
+  CmeanSpec cm{k_cache, k_rows, page_size, num_kv_heads, loc, nnz};
+  return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
+                    sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
+                    sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
+                    head_dim, seg_counters, seg_counters_len, mode, &cm, stream);
+}
+
+namespace {
+
+int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* x, uint16_t* x_out,
+               const uint16_t* y, int64_t y_rows, uint16_t* score, int64_t score_len,
+               const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+               int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+               int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
+               int32_t max_num_pages, int32_t head_dim, int32_t* seg_counters, int64_t seg_counters_len,
+               int32_t mode, const CmeanSpec* cms, void* stream) {
   if (eff_batch_size < 0 || group_size < 0 || reserved_bos < 0 || reserved_eos < 0)
     return vtx::fail(VTX_E_INVALID, "indexer_fused: negative size");
   if (!vtx_indexer_fused_supported(head_dim))
@@ -490,6 +772,16 @@ extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t grou
   // CUs idle, so their pages are split over several workgroups.
   const bool split = mode == VTX_FUSED_SPLIT ||
                      (mode == VTX_FUSED_AUTO && have_counters && (long long)eff_batch_size < 2LL * cus);
+  // The CMean runs inside the segment-layout launch for rows of one 16-byte
+  // vector per lane (its tile layout is then the scoring layout) and decode
+  // sized loc; otherwise as its own launch, first.
+  const bool cm_inside = cms && !split && (head_dim == 64 || head_dim == 128) && cms->nnz <= kCmLoc;
+  if (cms && !cm_inside && cms->nnz > 0) {
+    const int rc = vtx_page_reduce(cms->k, cms->k_rows, cms->page_size, head_dim, const_cast<uint16_t*>(y),
+                                   VTX_DTYPE_BF16, y_rows, cms->loc, cms->nnz, cms->heads, cms->page_size, 1,
+                                   VTX_REDUCE_MEAN, stream);
+    if (rc != VTX_OK) return rc;
+  }
   if (split) {
     // Small chunks when every segment's chunks fit on the chip at once
     // (four split workgroups per CU), else twice as large; past that,
@@ -526,8 +818,26 @@ extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t grou
   // segments only write their mean).
   const long long grid = a.x_out ? q_rows : eff_batch_size;
   if (grid > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many query rows");
-  if (grid == 0) return VTX_OK;
-  if (max_num_pages <= 256) return launch_dim<256>(a, (int)grid, lds, s);
-  if (max_num_pages <= 1024) return launch_dim<512>(a, (int)grid, lds, s);
-  return launch_dim<1024>(a, (int)grid, lds, s);
+  CmArgs cma{};
+  const bool cm_launch = cm_inside && cms->nnz > 0;
+  if (cm_launch) {  // the tiles are spread over the launch's own waves
+    cma.x = cms->k;
+    cma.x_rows = cms->k_rows;
+    cma.rows_per_tile = cms->page_size;
+    cma.cols = head_dim;
+    cma.out = const_cast<uint16_t*>(y);
+    cma.out_rows = y_rows;
+    cma.loc = cms->loc;
+    cma.nnz = cms->nnz;
+    cma.heads = cms->heads;
+    cma.page = cms->page_size;
+  }
+  const long long blocks = grid;
+  if (blocks == 0) return VTX_OK;
+  const CmArgs* cmp = cm_launch ? &cma : nullptr;
+  if (max_num_pages <= 256) return launch_dim<256>(a, cmp, (int)blocks, lds, s);
+  if (max_num_pages <= 1024) return launch_dim<512>(a, cmp, (int)blocks, lds, s);
+  return launch_dim<1024>(a, cmp, (int)blocks, lds, s);
 }
+
+}  // namespace

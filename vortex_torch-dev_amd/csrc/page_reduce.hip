@@ -21,76 +21,25 @@
 //     so CMean + CMax read K once.
 #include "vtx_device.h"
 #include "vtx_host.h"
+#include "vtx_page_reduce.h"
 
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / vtx::kWave;
-constexpr int kMaxOut = 4;
-
-struct ReduceArgs {
-  const uint16_t* x;
-  int64_t x_rows;
-  int32_t rows_per_tile;  // R
-  int32_t cols;           // C
-  void* out[kMaxOut];
-  int32_t out_dtype[kMaxOut];
-  int32_t out_type[kMaxOut];
-  int32_t n_out;
-  int64_t out_rows;
-  const int64_t* loc;
-  int64_t nnz;
-  int32_t heads;
-  int32_t page;
-};
-
-struct Acc {
-  float sum, sq, mx, mn;
-};
-
-// Statistics a launch needs (bit mask): only these are accumulated and
-// folded across lanes.
-constexpr int kNeedSum = 1, kNeedMax = 2, kNeedMin = 4, kNeedSq = 8, kNeedAll = 15;
-
-__host__ __device__ constexpr int need_of(int type) {
-  return type == VTX_REDUCE_MEAN ? kNeedSum
-         : type == VTX_REDUCE_MAX ? kNeedMax
-         : type == VTX_REDUCE_MIN ? kNeedMin
-                                  : kNeedSq;
-}
-
-template <int NEED = kNeedAll>
-__device__ __forceinline__ void acc_init(Acc& a) {
-  a.sum = 0.f;
-  a.sq = 0.f;
-  a.mx = -INFINITY;
-  a.mn = INFINITY;
-}
-template <int NEED = kNeedAll>
-__device__ __forceinline__ void acc_add(Acc& a, float v) {
-  if constexpr ((NEED & kNeedSum) != 0) a.sum += v;
-  if constexpr ((NEED & kNeedSq) != 0) a.sq = fmaf(v, v, a.sq);
-  if constexpr ((NEED & kNeedMax) != 0) a.mx = fmaxf(a.mx, v);
-  if constexpr ((NEED & kNeedMin) != 0) a.mn = fminf(a.mn, v);
-}
-template <int NEED = kNeedAll>
-__device__ __forceinline__ void acc_merge_xor(Acc& a, int d) {
-  if constexpr ((NEED & kNeedSum) != 0) a.sum += __shfl_xor(a.sum, d, vtx::kWave);
-  if constexpr ((NEED & kNeedSq) != 0) a.sq += __shfl_xor(a.sq, d, vtx::kWave);
-  if constexpr ((NEED & kNeedMax) != 0) a.mx = fmaxf(a.mx, __shfl_xor(a.mx, d, vtx::kWave));
-  if constexpr ((NEED & kNeedMin) != 0) a.mn = fminf(a.mn, __shfl_xor(a.mn, d, vtx::kWave));
-}
-// Final value of reduction `type` over `count` elements, rounded to bf16 bits.
-__device__ __forceinline__ uint32_t acc_value(const Acc& a, int type, int count) {
-  float v;
-  switch (type) {
-    case VTX_REDUCE_MEAN: v = a.sum / (float)count; break;
-    case VTX_REDUCE_MAX: v = a.mx; break;
-    case VTX_REDUCE_MIN: v = a.mn; break;
-    default: v = sqrtf(a.sq); break;
-  }
-  return vtx::f32_to_bf16(v);
-}
+constexpr int kMaxOut = vtx::kPageReduceMaxOut;
+using ReduceArgs = vtx::PageReduceArgs;
+using vtx::Acc;
+using vtx::acc_add;
+using vtx::acc_init;
+using vtx::acc_merge_xor;
+using vtx::acc_value;
+using vtx::kNeedAll;
+using vtx::kNeedMax;
+using vtx::kNeedMin;
+using vtx::kNeedSq;
+using vtx::kNeedSum;
+using vtx::need_of;
 
 __device__ __forceinline__ void store_one(const ReduceArgs& a, int o, long long elem, uint32_t bits) {
   if (a.out_dtype[o] == VTX_DTYPE_BF16)
@@ -99,39 +48,16 @@ __device__ __forceinline__ void store_one(const ReduceArgs& a, int o, long long 
     reinterpret_cast<uint32_t*>(a.out[o])[elem] = bits << 16;
 }
 
-// Collects the first tile row (page * H) of every page closed by this block's
-// loc entries, in loc order (the workgroups that share a block of entries
-// split its tiles by index, so they must all see the same list); returns the
-// page count.
+// The pages closed by this block's 256 loc entries (the workgroups that share
+// a block of entries split its tiles by index, so they all see the same list).
 __device__ __forceinline__ int collect_pages(const ReduceArgs& a, long long* first_row, int* wave_count) {
-  const int lane = vtx::lane_id();
-  const int wave = threadIdx.x / vtx::kWave;
-  const long long e = (long long)blockIdx.x * kThreads + threadIdx.x;
-  long long pos = 0;
-  bool closes = false;
-  if (e < a.nnz) {
-    pos = a.loc[e];
-    closes = (pos + 1) % a.page == 0;
-  }
-  const uint64_t m = __ballot(closes);
-  if (lane == 0) wave_count[wave] = __popcll(m);
-  __syncthreads();
-  int before = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < kWavesPerBlock; ++w) {
-    before += (w < wave) ? wave_count[w] : 0;
-    total += wave_count[w];
-  }
-  if (closes) first_row[before + vtx::lanes_below(m)] = (pos / a.page) * a.heads;
-  __syncthreads();
-  return total;
+  return vtx::collect_pages<kThreads>(a, (long long)blockIdx.x * kThreads, first_row, wave_count);
 }
 
 // dim 1, C = 8 * LPR with LPR | 64: lane = (row group, 16-byte column vector).
 // NEED: statistics to accumulate (kNeed* mask covering every output's type).
 template <int LPR, int NEED>
 __global__ __launch_bounds__(kThreads) void reduce_rows_vec_kernel(ReduceArgs a) {
-  constexpr int kGroups = vtx::kWave / LPR;
   __shared__ long long first_row[kThreads];
   __shared__ int wave_count[kWavesPerBlock];
   const int pages = collect_pages(a, first_row, wave_count);
@@ -144,46 +70,10 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_vec_kernel(ReduceArgs a)
 
   for (int t = blockIdx.y * kWavesPerBlock + wave; t < tiles; t += gridDim.y * kWavesPerBlock) {
     const long long row = first_row[t / a.heads] + (t % a.heads);
-    if (row < 0 || row >= a.x_rows || row >= a.out_rows) continue;
-    const uint16_t* base = a.x + row * (long long)R * a.cols + cv * 8;
+    if (!vtx::tile_in_range(a, row)) continue;
     Acc acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc_init<NEED>(acc[e]);
-#pragma unroll 4
-    for (int r = grp; r < R; r += kGroups) {
-      const vtx::U4 v = vtx::ld16_stream(base + (long long)r * a.cols);
-      acc_add<NEED>(acc[0], vtx::bf16_lo(v.x));
-      acc_add<NEED>(acc[1], vtx::bf16_hi(v.x));
-      acc_add<NEED>(acc[2], vtx::bf16_lo(v.y));
-      acc_add<NEED>(acc[3], vtx::bf16_hi(v.y));
-      acc_add<NEED>(acc[4], vtx::bf16_lo(v.z));
-      acc_add<NEED>(acc[5], vtx::bf16_hi(v.z));
-      acc_add<NEED>(acc[6], vtx::bf16_lo(v.w));
-      acc_add<NEED>(acc[7], vtx::bf16_hi(v.w));
-    }
-#pragma unroll
-    for (int d = LPR; d < vtx::kWave; d <<= 1)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc_merge_xor<NEED>(acc[e], d);
-    if (grp == 0) {
-      const long long elem = row * a.cols + cv * 8;
-#pragma unroll
-      for (int o = 0; o < kMaxOut; ++o) {
-        if (o >= a.n_out) break;
-        uint32_t b[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) b[e] = acc_value(acc[e], a.out_type[o], R);
-        if (a.out_dtype[o] == VTX_DTYPE_BF16) {
-          vtx::st16(reinterpret_cast<uint16_t*>(a.out[o]) + elem,
-                    vtx::U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
-                            b[6] | (b[7] << 16)});
-        } else {
-          uint32_t* dst = reinterpret_cast<uint32_t*>(a.out[o]) + elem;
-          vtx::st16(dst, vtx::U4{b[0] << 16, b[1] << 16, b[2] << 16, b[3] << 16});
-          vtx::st16(dst + 4, vtx::U4{b[4] << 16, b[5] << 16, b[6] << 16, b[7] << 16});
-        }
-      }
-    }
+    vtx::tile_stats_vec<LPR, NEED>(a.x, row, R, a.cols, grp, cv, acc);
+    if (grp == 0) vtx::tile_store_vec(a, row, cv, acc);
   }
 }
 

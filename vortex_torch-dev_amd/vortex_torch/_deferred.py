@@ -155,9 +155,94 @@ def current_scope() -> Optional[Scope]:
     return getattr(_tls, "scope", None)
 
 
+# ---------------------------------------------------------------- the carry
+# forward_cache's page-finish mean may be left unlaunched when the method
+# returns (the *carry*), for the next forward_indexer to run inside its fused
+# launch (vtx_indexer_fused_cmean).  It is launched on its own, on the stream
+# it was recorded on, as soon as anything else could observe it:
+#   * any other kernel launch of this package (every _hip wrapper checks);
+#   * any torch operation on a layout-tagged tensor (vTensor) that shares
+#     storage with the K pool, the centroid pool or loc;
+#   * the start of the next forward_cache;
+#   * the end of the forward_indexer that did not consume it.
+# So a carried mean is never read or overwritten before it is computed,
+# provided the centroid pool and the K pool are only touched through this
+# package or through torch on their vTensors between the two calls — as in
+# a decode layer, where forward_indexer follows forward_cache.
+
+
+def _carry_enabled() -> bool:
+    return fusion_enabled() and os.environ.get("VORTEX_FUSE_CMEAN", "1") != "0"
+
+
+def current_carry():
+    return getattr(_tls, "carry", None)
+
+
+def _stream_of(dev: torch.device):
+    return torch.cuda.current_stream(dev) if dev.type == "cuda" else None
+
+
+def flush_carry() -> None:
+    """Launches the carried page-finish mean, if any, on its own stream."""
+    c = current_carry()
+    if c is None:
+        return
+    _tls.carry = None
+    pending, stream = c
+    with (torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()):
+        pending.flush()
+
+
+def _storages(obj, out):
+    if isinstance(obj, torch.Tensor):
+        with torch._C.DisableTorchFunctionSubclass():
+            out.add(obj.untyped_storage().data_ptr())
+    elif isinstance(obj, (list, tuple)):
+        for x in obj:
+            _storages(x, out)
+    elif isinstance(obj, dict):
+        for x in obj.values():
+            _storages(x, out)
+    return out
+
+
+def carry_touched_by(args, kwargs) -> bool:
+    """Whether a torch call with these arguments uses the storage of the
+    carried mean's pool, output or loc."""
+    c = current_carry()
+    if c is None:
+        return False
+    mine = _storages([c[0].x, c[0].outs, c[0].loc], set())
+    return bool(mine & _storages([args, kwargs or {}], set()))
+
+
+def take_carry(y: torch.Tensor):
+    """The carried page-finish mean if it writes the centroid pool `y` and
+    was recorded on the current stream (the caller then runs it); None
+    otherwise (anything carried is launched first)."""
+    c = current_carry()
+    if c is None:
+        return None
+    pending, stream = c
+    with torch._C.DisableTorchFunctionSubclass():
+        same = (pending.outs[0].data_ptr() == y.data_ptr() and pending.outs[0].shape == y.shape
+                and _stream_of(y.device) == stream)
+    if not same:
+        flush_carry()
+        return None
+    _tls.carry = None
+    return pending
+
+
 @contextlib.contextmanager
-def scope(active: bool):
-    """Deferral scope; flushes everything still pending on exit."""
+def scope(active: bool, kind: str = "indexer"):
+    """Deferral scope; flushes everything still pending on exit.  kind
+    "cache" (forward_cache) may leave a page-finish mean as the carry;
+    kind "indexer" (forward_indexer) may consume it and launches it at exit
+    if it did not."""
+    if active and kind == "cache":
+        flush_carry()
     prev = current_scope()
     sc = Scope() if active else None
     _tls.scope = sc
@@ -166,7 +251,13 @@ def scope(active: bool):
     finally:
         _tls.scope = prev
         if sc is not None:
+            if (kind == "cache" and _carry_enabled() and len(sc.pending) == 1
+                    and getattr(sc.pending[0], "carryable", lambda: False)()):
+                p = sc.pending.pop()
+                _tls.carry = (p, _stream_of(p.x.device))
             sc.flush()
+            if kind == "indexer":
+                flush_carry()
 
 
 def flush_all() -> None:
@@ -291,3 +382,12 @@ def plain(t: torch.Tensor) -> torch.Tensor:
     make an elided result look observed."""
     with torch._C.DisableTorchFunctionSubclass():
         return torch.Tensor._make_subclass(torch.Tensor, t, require_grad=False)
+
+
+def _install_launch_hook() -> None:
+    from . import _hip
+
+    _hip.set_pre_launch_hook(flush_carry)
+
+
+_install_launch_hook()

@@ -61,6 +61,11 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
+    "vtx_indexer_fused_cmean": (
+        [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _vp],
+        ctypes.c_int,
+    ),
     "vtx_indexer_gqa_fused": (
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
          _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp],
@@ -171,7 +176,19 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"vortex_torch HIP {what} failed (code {rc}): {msg}")
 
 
+_pre_launch = None
+
+
+def set_pre_launch_hook(fn) -> None:
+    """fn() runs before every launch of this module (the deferral layer uses
+    it to launch recorded work that a new launch could observe)."""
+    global _pre_launch
+    _pre_launch = fn
+
+
 def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    if _pre_launch is not None:
+        _pre_launch()
     dev = None
     for t in tensors:
         if t.device.type != "cuda":
@@ -510,6 +527,7 @@ def indexer_fused(
     max_num_pages: int,
     seg_counters=None,
     mode: int = FUSED_AUTO,
+    cmean=None,
 ) -> None:
     """q-mean + GeMV + topK of one layer in one launch.
 
@@ -519,10 +537,15 @@ def indexer_fused(
     output buffer; the block tables come from the planner.  seg_counters: an
     int32 buffer of at least S zeros that lets long segments be split over
     several workgroups (the kernel leaves it zeroed); mode: FUSED_AUTO,
-    FUSED_SEGMENT or FUSED_SPLIT.
+    FUSED_SEGMENT or FUSED_SPLIT.  cmean: (k_cache [rows, P, D] bf16, loc
+    int64, num_kv_heads) — the layer's page-finish mean into y, run first in
+    the same launch (``vtx_indexer_fused_cmean``), with the results of a
+    separate ``page_reduce`` launch before this one.
     """
     lib = load_library()
     tensors = [q, y, score, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
+    if cmean is not None:
+        tensors += [cmean[0], cmean[1]]
     if x_out is not None:
         tensors.append(x_out)
     if seg_counters is not None:
@@ -551,9 +574,7 @@ def indexer_fused(
         if x_out.numel() < S * D:
             raise RuntimeError("vortex_torch: q_mean output too small")
     averaged = G == 1 and x_out is None
-    with _on_device(dev):
-        rc = lib.vtx_indexer_fused(
-            None if averaged else q.data_ptr(), S, 0 if averaged else G,
+    args = (None if averaged else q.data_ptr(), S, 0 if averaged else G,
             q.data_ptr() if averaged else None,
             x_out.data_ptr() if x_out is not None else None,
             y.data_ptr(), y.numel() // D, score.data_ptr(), score.numel(),
@@ -562,8 +583,21 @@ def indexer_fused(
             sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), D,
             seg_counters.data_ptr() if seg_counters is not None else None,
-            seg_counters.numel() if seg_counters is not None else 0, int(mode),
-            _stream(dev))
+            seg_counters.numel() if seg_counters is not None else 0, int(mode))
+    if cmean is not None:
+        k, loc, heads = cmean
+        _req(k, torch.bfloat16, "k_cache")
+        _req(loc, torch.int64, "loc")
+        if k.dim() != 3 or int(k.shape[2]) != D or int(y.shape[1]) != 1:
+            raise RuntimeError(f"vortex_torch: CMean pool {tuple(k.shape)} / centroids {tuple(y.shape)} "
+                               f"do not match head_dim {D}")
+        with _on_device(dev):
+            rc = lib.vtx_indexer_fused_cmean(*args, k.data_ptr(), int(k.shape[0]), int(k.shape[1]), int(heads),
+                                             loc.data_ptr(), loc.numel(), _stream(dev))
+        _check(rc, "indexer_fused_cmean")
+        return
+    with _on_device(dev):
+        rc = lib.vtx_indexer_fused(*args, _stream(dev))
     _check(rc, "indexer_fused")
 
 

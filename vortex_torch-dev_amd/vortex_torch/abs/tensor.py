@@ -127,6 +127,8 @@ class vTensor(torch.Tensor):
             if deferred is not None:
                 return deferred
             d.flush_all()
+        if d.current_carry() is not None and not d.is_metadata(func) and d.carry_touched_by(args, kwargs):
+            d.flush_carry()  # a carried page-finish mean reads or writes these
         fmt = _op_format(args, kwargs)
         with torch._C.DisableTorchFunctionSubclass():
             out = func(*args, **kwargs)

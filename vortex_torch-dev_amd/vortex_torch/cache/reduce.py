@@ -74,6 +74,23 @@ class _PendingPageReduce(_deferred.Pending):
         self.outs.append(out)
         self.types.append(kernel_type)
 
+    #: loc entries the fused indexer launch scans for a carried mean
+    CARRY_MAX_LOC = 256
+
+    def carryable(self) -> bool:
+        """Whether the next forward_indexer's fused launch may run this record
+        (vtx_indexer_fused_cmean): a single decode-sized mean (dim 1) of
+        [page_size, D] tiles into a bf16 [rows, 1, D] centroid pool."""
+        if self.done or len(self.outs) != 1 or self.types[0] != _hip.REDUCE_MEAN or self.dim != 1:
+            return False
+        out, x = self.outs[0], self.x
+        if not _recordable_operands(x, out, self.loc):
+            return False
+        with torch._C.DisableTorchFunctionSubclass():
+            return (out.dtype == torch.bfloat16 and out.dim() == 3 and x.dim() == 3
+                    and int(out.shape[1]) == 1 and int(x.shape[2]) == int(out.shape[2])
+                    and int(x.shape[1]) == int(self.ctx.page_size) and self.loc.numel() <= self.CARRY_MAX_LOC)
+
     def _run(self) -> None:
         c = self.ctx
         if len(self.outs) == 1:

@@ -34,7 +34,7 @@ def _ctx_of(args, kwargs, pos: int):
     return args[pos] if len(args) > pos else None
 
 
-def _scoped(fn, ctx_pos: int):
+def _scoped(fn, ctx_pos: int, kind: str):
     """Runs a forward_indexer / forward_cache inside a deferral scope when its
     context is in execute mode (see vortex_torch._deferred): recorded work is
     fused where possible and everything is finished when the method returns.
@@ -44,7 +44,7 @@ def _scoped(fn, ctx_pos: int):
     def scoped(self, *args, **kwargs):
         ctx = _ctx_of(args, kwargs, ctx_pos)
         mode = getattr(ctx, "mode", None)
-        with _deferred.scope(active=mode is None or mode == Mode.execute):
+        with _deferred.scope(active=mode is None or mode == Mode.execute, kind=kind):
             return fn(self, *args, **kwargs)
 
     scoped._vtx_scoped = True
@@ -57,10 +57,10 @@ class vFlow(ABC):
 
     def __init_subclass__(cls, **kwargs):
         super().__init_subclass__(**kwargs)
-        for name, ctx_pos in (("forward_indexer", 3), ("forward_cache", 2)):
+        for name, ctx_pos, kind in (("forward_indexer", 3, "indexer"), ("forward_cache", 2, "cache")):
             fn = cls.__dict__.get(name)
             if fn is not None and not getattr(fn, "_vtx_scoped", False) and callable(fn):
-                setattr(cls, name, _scoped(fn, ctx_pos))
+                setattr(cls, name, _scoped(fn, ctx_pos, kind))
 
     @abstractmethod
     def forward_indexer(self, q: torch.Tensor, o: torch.Tensor, cache: Dict[str, torch.Tensor],

@@ -58,12 +58,18 @@ class PendingGemv(_deferred.Pending):
         else:
             _deferred.materialize(self.x)
             q, x_out, mean = self.x, None, None
+        # the page-finish mean forward_cache left for these centroids runs in
+        # the same launch (its results, then these)
+        cm = _deferred.take_carry(self.y)
         _hip.indexer_fused(
             q, x_out, self.y, self.op.output_buffer,
             ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
             ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
             ctx.page_reserved_eos, ctx.max_num_pages_per_request, seg_counters=seg_counters,
-            mode=_deferred.fused_layout())
+            mode=_deferred.fused_layout(),
+            cmean=None if cm is None else (cm.x, cm.loc, cm.ctx.head_num))
+        if cm is not None:
+            cm.done = True
         if mean is not None:
             mean.done = True
         self.done = True
