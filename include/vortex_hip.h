@@ -263,6 +263,28 @@ int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                           int32_t reserved_eos, int32_t max_num_pages, int32_t softmax,
                           float scale, void* stream);
 
+/*
+ * vtx_indexer_gqa_fused preceded by the layer's page-finish mean into y: the
+ * results of vtx_page_reduce(k_cache, k_rows, page_size, head_dim, y, BF16,
+ * y_rows, loc, nnz, num_kv_heads, page_size, 1, VTX_REDUCE_MEAN) followed by
+ * vtx_indexer_gqa_fused with the same arguments, bit for bit (y is written).
+ * No single counterpart in the reference: CMean (the cache step of
+ * gqa_block_sparse_attention, vortex_torch/flow/algorithms.py:238-352) and
+ * the layer's GQA indexer step in one launch, for head_dim 64 / 128 and
+ * nnz <= 256 (otherwise the mean is its own launch, first).
+ */
+int vtx_indexer_gqa_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                                uint16_t* y, int64_t y_rows, int32_t head_dim,
+                                uint16_t* score, int64_t score_rows, uint16_t* aggr, int64_t aggr_len,
+                                const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                                const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                                int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                                int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                                int32_t reserved_eos, int32_t max_num_pages, int32_t softmax,
+                                float scale, const uint16_t* k_cache, int64_t k_rows,
+                                int32_t page_size, int32_t num_kv_heads, const int64_t* loc,
+                                int64_t nnz, void* stream);
+
 /* 1 if vtx_indexer_gqa_fused handles this head_dim and group size. */
 int vtx_indexer_gqa_fused_supported(int32_t head_dim, int32_t group_size);
 

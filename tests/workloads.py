@@ -243,3 +243,37 @@ def k_pool(batch: DecodeBatch, seed: int, device, page_offsets: bool = False) ->
                           device=device, dtype=torch.float32) * (0.5 ** 0.5)
         k.add_(off)
     return k.to(torch.bfloat16)
+
+
+def cmean_case(name: str):
+    """(batch, loc) for a fused launch that runs the layer's CMean: decode
+    configurations and layouts where the closed pages are scored (eos 0, or
+    loc slots closing middle pages), plus the cases that fall back to a
+    page-reduce launch of their own (more loc entries than one launch scans,
+    head_dim 256)."""
+    if name == "eos0":  # every request's last page closes and is a middle page (eos 0)
+        b = make_batch([1024, 2048, 640, 4096, 512], pool_pages=900, seed=21, eos=0, topk=12)
+        return b, decode_loc(b)
+    if name == "mid":  # closing slots of middle pages, several per request
+        b = make_batch([3000, 5000, 1800], pool_pages=700, seed=22, topk=20)
+        g = torch.Generator().manual_seed(5)
+        slots = []
+        for pages in b.pages:
+            pick = torch.randperm(len(pages) - 2, generator=g)[:9] + 1
+            slots += [int(pages[i]) * b.page_size + b.page_size - 1 for i in pick]
+        slots += [7, 16 * 3 + 2]  # tokens that close nothing
+        return b, torch.as_tensor(slots, dtype=torch.int64)
+    if name == "d64":
+        b = make_batch([3000, 1500, 700], pool_pages=400, seed=23, head_dim=64, group_size=1, eos=0)
+        return b, decode_loc(b)
+    if name == "big_loc":  # more loc entries than one launch scans: CMean launched first
+        b = make_batch([4096, 4096], pool_pages=600, seed=24)
+        return b, torch.arange(300, dtype=torch.int64) * 3
+    if name == "d256":  # wider rows: CMean launched first
+        b = make_batch([2000, 3000], pool_pages=400, seed=25, head_dim=256, eos=0)
+        return b, decode_loc(b)
+    if name.startswith("r"):
+        b = random_small(int(name[1:]))
+        return b, decode_loc(b)
+    b = globals()[name]()
+    return b, decode_loc(b)

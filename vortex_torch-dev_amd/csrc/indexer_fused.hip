@@ -35,13 +35,13 @@
 // kernel's for the same query.
 #include "vtx_device.h"
 #include "vtx_host.h"
+#include "vtx_cmean.h"
 #include "vtx_page_reduce.h"
 #include "vtx_score.h"
 #include "vtx_select.h"
 
 namespace {
 
-constexpr int kCmLoc = 256;  // loc entries a launch with an in-kernel CMean scans
 
 struct FusedArgs {
   const uint16_t* q;  // [S, G, D] when G > 0
@@ -65,140 +65,6 @@ struct FusedArgs {
   int32_t row_cap;   // segments up to this many middle pages are held in LDS
   int32_t segments;  // eff_batch_size; the grid covers all q_rows
 };
-
-// The layer's decode CMean run inside a fused launch (kCm): the mean over
-// each closed page's [rows_per_tile, cols] K tile into y (`out`), whose
-// rows are the centroids the launch scores — a scored page that this CMean
-// closes is scored against its fresh centroid (fresh_score).
-struct CmArgs {
-  const uint16_t* x;  // K pool [x_rows, rows_per_tile, cols]
-  int64_t x_rows;
-  int32_t rows_per_tile, cols;
-  uint16_t* out;      // == y
-  int64_t out_rows;
-  const int64_t* loc;
-  int64_t nnz;
-  int32_t heads, page;
-};
-
-// The pages this launch's CMean closes, as one wave holds them (no LDS, no
-// barrier): lane l keeps, for loc entries j * 64 + l (j < kLocRegs), the
-// first tile row (page * H) of the page the entry closes, or -1; mask[j] is
-// the ballot of the closing entries, so "the i-th closed page" is the i-th
-// set bit in loc order, the order the page-reduce kernel lists them in.
-template <int kLocRegs>
-struct Closing {
-  int base[kLocRegs];
-  uint64_t mask[kLocRegs];
-  int count;
-};
-
-template <int kLocRegs>
-__device__ __forceinline__ void closing_load(const CmArgs& cm, long long (&pos)[kLocRegs]) {
-  const int lane = vtx::lane_id();
-#pragma unroll
-  for (int j = 0; j < kLocRegs; ++j) {
-    const long long e = (long long)j * vtx::kWave + lane;
-    pos[j] = e < cm.nnz ? cm.loc[e] : 0;
-  }
-}
-
-template <int kLocRegs>
-__device__ __forceinline__ Closing<kLocRegs> closing_build(const CmArgs& cm, const long long (&pos)[kLocRegs]) {
-  const int lane = vtx::lane_id();
-  Closing<kLocRegs> c;
-  c.count = 0;
-#pragma unroll
-  for (int j = 0; j < kLocRegs; ++j) {
-    const long long e = (long long)j * vtx::kWave + lane;
-    const bool closes = e < cm.nnz && (pos[j] + 1) % cm.page == 0;  // C semantics, as page-reduce
-    c.base[j] = closes ? (int)((pos[j] / cm.page) * cm.heads) : -1;
-    c.mask[j] = __ballot(closes);
-    c.count += __popcll(c.mask[j]);
-  }
-  return c;
-}
-
-// First tile row of the i-th closed page (i < c.count); wave-uniform i.
-template <int kLocRegs>
-__device__ __forceinline__ int closing_base(const Closing<kLocRegs>& c, int i) {
-#pragma unroll
-  for (int j = 0; j < kLocRegs; ++j) {
-    const int n = __popcll(c.mask[j]);
-    if (i < n) {
-      uint64_t m = c.mask[j];
-      for (int k = 0; k < i; ++k) m &= m - 1;
-      return __builtin_amdgcn_readlane(c.base[j], __ffsll((long long)m) - 1);
-    }
-    i -= n;
-  }
-  return -1;
-}
-
-// Tiles first, first + stride, ... of the closed pages (tile t: head t % H
-// of closed page t / H): the mean over each tile's rows into cm.out, exactly
-// as reduce_rows_vec_kernel<LPR, kNeedSum> computes it.  Wave-level.
-template <int LPR, int kLocRegs>
-__device__ __forceinline__ void cmean_tiles(const CmArgs& cm, const Closing<kLocRegs>& c, int first, int stride,
-                                            int grp, int cv) {
-  const int tiles = c.count * cm.heads;
-  for (int t = first; t < tiles; t += stride) {
-    const long long row = (long long)closing_base(c, t / cm.heads) + (t % cm.heads);
-    if (!vtx::tile_in_range(cm, row)) continue;
-    vtx::Acc acc[8];
-    vtx::tile_stats_vec<LPR, vtx::kNeedSum>(cm.x, row, cm.rows_per_tile, cm.cols, grp, cv, acc);
-    if (grp == 0) {
-      uint32_t bb[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bb[e] = vtx::acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
-      vtx::st16(cm.out + row * cm.cols + cv * 8, vtx::U4{bb[0] | (bb[1] << 16), bb[2] | (bb[3] << 16),
-                                                        bb[4] | (bb[5] << 16), bb[6] | (bb[7] << 16)});
-    }
-  }
-}
-
-// Score of tile row `rid` against the freshly reduced centroid, for a page
-// the in-kernel CMean closes (the row in y may not be written yet): the
-// wave recomputes the centroid from the page's K tile with the CMean's own
-// arithmetic and scores it with the lane's dot_row chain and the xor tree
-// over the LPR lanes — the bits score_pass gives for that centroid row.
-// All 64 lanes take part and all return the score.  Rows of one 16-byte
-// vector per lane (VPL == 1).
-template <int LPR>
-__device__ __forceinline__ float fresh_score(const CmArgs& cm, int rid, const float (&xs)[1][8],
-                                             int grp, int col) {
-  vtx::Acc acc[8];
-  vtx::tile_stats_vec<LPR, vtx::kNeedSum>(cm.x, rid, cm.rows_per_tile, cm.cols, grp, col, acc);
-  uint32_t b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = vtx::acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
-  const vtx::U4 cen[1] = {vtx::U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
-                                  b[6] | (b[7] << 16)}};
-  float f = vtx::dot_row<1>(cen, xs);
-#pragma unroll
-  for (int d = LPR / 2; d >= 1; d >>= 1) f += __shfl_xor(f, d, vtx::kWave);
-  return f;
-}
-
-// Whether the lane's pass position (r >= 0, row my_rid) is a tile the
-// in-kernel CMean writes: a row in [page * H, page * H + H) of a closed page,
-// inside the pool and the centroid pool.
-template <int kLocRegs>
-__device__ __forceinline__ bool closes_here(const CmArgs& cm, const Closing<kLocRegs>& c, int r, int my_rid) {
-  const bool cand = r >= 0 && my_rid >= 0 && my_rid < cm.x_rows && my_rid < cm.out_rows;
-  bool fix = false;
-#pragma unroll
-  for (int j = 0; j < kLocRegs; ++j) {
-    uint64_t m = c.mask[j];
-    while (m) {  // wave-uniform
-      const int l = __ffsll((long long)m) - 1;
-      m &= m - 1;
-      const int base = __builtin_amdgcn_readlane(c.base[j], l);
-      fix |= (unsigned)(my_rid - base) < (unsigned)cm.heads;
-    }
-  }
-  return cand && fix;
-}
 
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
 // fp32 mean of its G rows (torch's mean), or the row itself when G == 0.
@@ -269,7 +135,7 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
 
 // One workgroup per segment: scores into LDS, select in LDS.
 template <int T, int LPR, int VPL, int kCmRegs>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a, CmArgs cma) {
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a, vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   constexpr int kPass = vtx::segment_pass<VPL>();
@@ -286,7 +152,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int k = a.topk;
   const int D = a.dim;
   const bool store_mean = wave == 0 && grp == 0;
-  __shared__ int32_t fix_pos[kCmLoc];  // middle positions scored in step 4b
+  __shared__ int32_t fix_pos[vtx::kCmLoc];  // middle positions scored in step 4b
   __shared__ int fix_n;
   // kCmRegs > 0: this launch runs the layer's CMean over up to 64 * kCmRegs loc entries
   constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
@@ -295,7 +161,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // ---- 0. with the in-kernel CMean, loc (issued first, so that waiting for
   // it waits for nothing else; used once the first row ids are requested)
   long long cm_pos[kLocRegs];
-  if constexpr (cm_on) closing_load(cma, cm_pos);
+  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
 
   // ---- 1. query rows (issued first: only needed once centroid rows arrive)
   vtx::U4 qv[kQRegs][VPL];
@@ -318,7 +184,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     obase = (long long)a.sindptr[seg] + a.bos;
   }
   // pages the in-kernel CMean closes (its loc load overlaps the bounds')
-  Closing<kLocRegs> closing{};
+  vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
   bool active = is_seg && k > 0 && n > k;
   if (active && (start < 0 || start + n > a.score_len || start + n > a.didx_len || obase < 0 ||
@@ -344,7 +210,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     if (cm_on && tid == 0) fix_n = 0;
     __syncthreads();  // histogram cleared before any wave counts into it
     if constexpr (cm_on) {
-      closing = closing_build(cma, cm_pos);
+      closing = vtx::closing_build(cma, cm_pos);
       n_close = closing.count;
     }
 
@@ -365,7 +231,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       int r;
       const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
       const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
-      if (cm_on && n_close > 0 && closes_here(cma, closing, r, my_rid)) {
+      if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
         // the in-kernel CMean rewrites this page's centroid: scored after the loop
         fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);
         r = -1;
@@ -387,10 +253,10 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // its passes (the registers of the scoring loop are free by then).
   if constexpr (cm_on) {
     if (!active) {  // the closed pages
-      closing = closing_build(cma, cm_pos);
+      closing = vtx::closing_build(cma, cm_pos);
       n_close = closing.count;
     }
-    cmean_tiles<LPR, kLocRegs>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
+    vtx::cmean_tiles<LPR, kLocRegs>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
                                col);
     if (!active) return;
   }
@@ -404,7 +270,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       for (int i = wave; i < fix_n; i += kWaves) {
         const int pos = fix_pos[i];
         const int rid = dseg[pos];
-        const float f = fresh_score<LPR>(cma, rid, xs, grp, col);
+        const float f = vtx::score_vec<LPR>(vtx::fresh_centroid<LPR>(cma, rid, grp, col), xs);
         if (lane == 0) {
           const uint32_t sb = vtx::f32_to_bf16(f);
           const uint32_t key = vtx::score_key(sb);
@@ -585,18 +451,18 @@ constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS; the select tables take up
 constexpr int kMaxTopk = 4096;
 
 template <int T>
-int launch_dim(const FusedArgs& a, const CmArgs* cm, int blocks, size_t lds, hipStream_t s) {
-  const CmArgs none{};
+int launch_dim(const FusedArgs& a, const vtx::CmArgs* cm, int blocks, size_t lds, hipStream_t s) {
+  const vtx::CmArgs none{};
   if (cm) {  // the in-kernel CMean: rows of one 16-byte vector per lane
     const bool one = cm->nnz <= vtx::kWave;  // loc in one register per lane
     switch (a.dim) {
       case 64:
         if (one) indexer_fused_kernel<T, 8, 1, 1><<<blocks, T, lds, s>>>(a, *cm);
-        else indexer_fused_kernel<T, 8, 1, kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
+        else indexer_fused_kernel<T, 8, 1, vtx::kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
         break;
       case 128:
         if (one) indexer_fused_kernel<T, 16, 1, 1><<<blocks, T, lds, s>>>(a, *cm);
-        else indexer_fused_kernel<T, 16, 1, kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
+        else indexer_fused_kernel<T, 16, 1, vtx::kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
         break;
       default: return vtx::fail(VTX_E_INVALID, "indexer_fused: in-kernel CMean needs head_dim 64 or 128");
     }
@@ -775,7 +641,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   // The CMean runs inside the segment-layout launch for rows of one 16-byte
   // vector per lane (its tile layout is then the scoring layout) and decode
   // sized loc; otherwise as its own launch, first.
-  const bool cm_inside = cms && !split && (head_dim == 64 || head_dim == 128) && cms->nnz <= kCmLoc;
+  const bool cm_inside = cms && !split && (head_dim == 64 || head_dim == 128) && cms->nnz <= vtx::kCmLoc;
   if (cms && !cm_inside && cms->nnz > 0) {
     const int rc = vtx_page_reduce(cms->k, cms->k_rows, cms->page_size, head_dim, const_cast<uint16_t*>(y),
                                    VTX_DTYPE_BF16, y_rows, cms->loc, cms->nnz, cms->heads, cms->page_size, 1,
@@ -818,7 +684,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   // segments only write their mean).
   const long long grid = a.x_out ? q_rows : eff_batch_size;
   if (grid > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many query rows");
-  CmArgs cma{};
+  vtx::CmArgs cma{};
   const bool cm_launch = cm_inside && cms->nnz > 0;
   if (cm_launch) {  // the tiles are spread over the launch's own waves
     cma.x = cms->k;
@@ -834,7 +700,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   }
   const long long blocks = grid;
   if (blocks == 0) return VTX_OK;
-  const CmArgs* cmp = cm_launch ? &cma : nullptr;
+  const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
   if (max_num_pages <= 256) return launch_dim<256>(a, cmp, (int)blocks, lds, s);
   if (max_num_pages <= 1024) return launch_dim<512>(a, cmp, (int)blocks, lds, s);
   return launch_dim<1024>(a, cmp, (int)blocks, lds, s);

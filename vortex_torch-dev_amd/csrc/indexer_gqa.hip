@@ -15,6 +15,7 @@
 // kernels' output.  Segments with up to row_cap middle pages keep the raw
 // scores, keys and page ids in LDS; longer ones stage them in the output
 // buffers.
+#include "vtx_cmean.h"
 #include "vtx_device.h"
 #include "vtx_host.h"
 #include "vtx_score.h"
@@ -42,8 +43,12 @@ struct GqaArgs {
   float scale;
 };
 
-template <int T, int LPR, int VPL, int kG>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fused_kernel(GqaArgs a) {
+// kCmRegs > 0: the launch also runs the layer's decode CMean into y (loc: up
+// to 64 * kCmRegs entries, rows of one vector per lane), as the block-sparse
+// fused kernel does (vtx_cmean.h).
+template <int T, int LPR, int VPL, int kG, int kCmRegs>
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fused_kernel(GqaArgs a,
+                                                                                       vtx::CmArgs cma) {
   static_assert(T >= vtx::kScanThreads, "the softmax statistics need kScanThreads threads");
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
@@ -52,6 +57,11 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   __shared__ vtx::SelectShared<T> sh;
   __shared__ float pm[vtx::kScanThreads];
   __shared__ float ps[vtx::kScanThreads];
+
+  constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
+  constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
+  __shared__ int32_t fix_pos[vtx::kCmLoc];  // positions whose raw scores are redone (CMean)
+  __shared__ int fix_n;
 
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
@@ -63,24 +73,38 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   const int D = a.dim;
   const int G = a.G;
 
+  long long cm_pos[kLocRegs];
+  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
   const long long start = (long long)a.dindptr[seg] + a.bos;
   const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
   const long long obase = (long long)a.sindptr[seg] + a.bos;
-  if (!(k > 0 && n > k) || start < 0 || start + n > a.score_rows || start + n > a.aggr_len ||
-      start + n > a.didx_len || obase < 0 || obase + k > a.sidx_len)
-    return;  // uniform: the separate ops write nothing for this segment either
+  const bool active = k > 0 && n > k && start >= 0 && start + n <= a.score_rows && start + n <= a.aggr_len &&
+                      start + n <= a.didx_len && obase >= 0 && obase + k <= a.sidx_len;
+  if constexpr (!cm_on) {
+    if (!active) return;  // uniform: the separate ops write nothing for this segment either
+  }
   const bool cached = n <= a.row_cap;
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
   uint16_t* raw = keys + a.row_cap;  // [row_cap, G]
   uint16_t* sc_out = a.score + start * G;
-  vtx::select_init<T>(sel, k, sh);
-
-  // ---- scores of every middle page for every query head
   const int32_t* dseg = a.didx + start;
   const uint16_t* qs = a.q + (long long)seg * G * D;
-  long long share = (n + kWaves - 1) / kWaves;
+  vtx::Closing<kLocRegs> closing{};
+  int n_close = 0;
+  long long share = 0;
+  if (active) {  // uniform
+  vtx::select_init<T>(sel, k, sh);
+  if constexpr (cm_on) {
+    if (tid == 0) fix_n = 0;
+    __syncthreads();
+    closing = vtx::closing_build(cma, cm_pos);
+    n_close = closing.count;
+  }
+
+  // ---- scores of every middle page for every query head
+  share = (n + kWaves - 1) / kWaves;
   share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
   if (share > kPass) share = kPass;
   for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
@@ -114,8 +138,40 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     }
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
     if (cached && r >= 0) rows[p0 + r] = my_rid;
+    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid))
+      fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);  // its scores are redone after the loop
+  }
+  }  // active
+  // this launch's CMean: wave w of workgroup b reduces tiles w * grid + b, ...
+  if constexpr (cm_on) {
+    if (!active) closing = vtx::closing_build(cma, cm_pos);
+    vtx::cmean_tiles<LPR, kLocRegs>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x,
+                                    kWaves * (int)gridDim.x, grp, col);
+    if (!active) return;
   }
   __syncthreads();
+
+  // ---- pages whose centroid this launch's CMean rewrites: their raw scores
+  // against the recomputed centroid, a wave each
+  if constexpr (cm_on) {
+    if (n_close > 0 && fix_n > 0) {  // uniform
+      for (int i = wave; i < fix_n; i += kWaves) {
+        const int pos = fix_pos[i];
+        const vtx::U4 cen = vtx::fresh_centroid<LPR>(cma, dseg[pos], grp, col);
+        for (int g = 0; g < G; ++g) {
+          float xg[1][8];
+          vtx::unpack8(vtx::ld16(qs + (long long)g * D + col * 8), xg[0]);
+          const float f = vtx::score_vec<LPR>(cen, xg);
+          if (lane == 0) {
+            const uint16_t b = (uint16_t)vtx::f32_to_bf16(f);
+            if (cached) raw[(long long)pos * G + g] = b;
+            else sc_out[(long long)pos * G + g] = b;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
 
   // ---- softmax statistics of each query head over the segment
   auto raw_at = [&](long long i, int g) -> float {
@@ -160,22 +216,38 @@ constexpr int kMaxTopk = 4096;
 constexpr int kMaxGroup = 8;
 
 template <int T, int kG>
-int launch_dim(const GqaArgs& a, int grid, size_t lds, hipStream_t s) {
+int launch_dim(const GqaArgs& a, const vtx::CmArgs* cm, int grid, size_t lds, hipStream_t s) {
+  const vtx::CmArgs none{};
+  if (cm) {  // the in-kernel CMean: rows of one 16-byte vector per lane
+    const bool one = cm->nnz <= vtx::kWave;
+    switch (a.dim) {
+      case 64:
+        if (one) gqa_fused_kernel<T, 8, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
+        else gqa_fused_kernel<T, 8, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        break;
+      case 128:
+        if (one) gqa_fused_kernel<T, 16, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
+        else gqa_fused_kernel<T, 16, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        break;
+      default: return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused: in-kernel CMean needs head_dim 64 or 128");
+    }
+    return vtx::check_launch("indexer_gqa_fused (with CMean)");
+  }
   switch (a.dim) {
-    case 64: gqa_fused_kernel<T, 8, 1, kG><<<grid, T, lds, s>>>(a); break;
-    case 128: gqa_fused_kernel<T, 16, 1, kG><<<grid, T, lds, s>>>(a); break;
-    case 256: gqa_fused_kernel<T, 16, 2, 1><<<grid, T, lds, s>>>(a); break;
+    case 64: gqa_fused_kernel<T, 8, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
+    case 128: gqa_fused_kernel<T, 16, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
+    case 256: gqa_fused_kernel<T, 16, 2, 1, 0><<<grid, T, lds, s>>>(a, none); break;
     // wide rows keep their query slice in registers: fewer threads, no spills
-    case 512: gqa_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1><<<grid, (T > 512 ? 512 : T), lds, s>>>(a); break;
-    case 576: gqa_fused_kernel<256, 8, 9, 1><<<grid, 256, lds, s>>>(a); break;
+    case 512: gqa_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1, 0><<<grid, (T > 512 ? 512 : T), lds, s>>>(a, none); break;
+    case 576: gqa_fused_kernel<256, 8, 9, 1, 0><<<grid, 256, lds, s>>>(a, none); break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_gqa_fused");
 }
 
 template <int T>
-int launch_g(const GqaArgs& a, int grid, size_t lds, hipStream_t s) {
-  return a.G >= 2 ? launch_dim<T, 2>(a, grid, lds, s) : launch_dim<T, 1>(a, grid, lds, s);
+int launch_g(const GqaArgs& a, const vtx::CmArgs* cm, int grid, size_t lds, hipStream_t s) {
+  return a.G >= 2 ? launch_dim<T, 2>(a, cm, grid, lds, s) : launch_dim<T, 1>(a, cm, grid, lds, s);
 }
 
 }  // namespace
@@ -184,6 +256,26 @@ extern "C" int vtx_indexer_gqa_fused_supported(int32_t head_dim, int32_t group_s
   return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512 || head_dim == 576) &&
          group_size >= 1 && group_size <= kMaxGroup;
 }
+
+namespace {
+
+// The decode CMean a GQA launch may run first (vtx_indexer_gqa_fused_cmean).
+struct CmeanSpec {
+  const uint16_t* k;
+  int64_t k_rows;
+  int32_t page_size, heads;
+  const int64_t* loc;
+  int64_t nnz;
+};
+
+int gqa_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* y, int64_t y_rows,
+             int32_t head_dim, uint16_t* score, int64_t score_rows, uint16_t* aggr, int64_t aggr_len,
+             const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+             int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+             int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
+             int32_t max_num_pages, int32_t softmax, float scale, const CmeanSpec* cms, void* stream);
+
+}  // namespace
 
 extern "C" int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* y,
                                      int64_t y_rows, int32_t head_dim, uint16_t* score, int64_t score_rows,
@@ -194,6 +286,41 @@ extern "C" int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t 
                                      int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
                                      int32_t softmax, float scale, void* stream) {
   vtx::clear_error();
+  return gqa_impl(q, q_rows, group_size, y, y_rows, head_dim, score, score_rows, aggr, aggr_len, dense_kv_indptr,
+                  sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices, sparse_kv_indices_len,
+                  eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, softmax, scale, nullptr,
+                  stream);
+}
+
+extern "C" int vtx_indexer_gqa_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size, uint16_t* y,
+                                           int64_t y_rows, int32_t head_dim, uint16_t* score, int64_t score_rows,
+                                           uint16_t* aggr, int64_t aggr_len, const int32_t* dense_kv_indptr,
+                                           const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+                                           int64_t dense_kv_indices_len, int32_t* sparse_kv_indices,
+                                           int64_t sparse_kv_indices_len, int32_t eff_batch_size, int32_t topk_val,
+                                           int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
+                                           int32_t softmax, float scale, const uint16_t* k_cache, int64_t k_rows,
+                                           int32_t page_size, int32_t num_kv_heads, const int64_t* loc,
+                                           int64_t nnz, void* stream) {
+  vtx::clear_error();
+  if (!k_cache || (nnz > 0 && !loc))
+    return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused_cmean: null K pool or loc");
+  if (page_size < 1 || num_kv_heads < 1 || k_rows < 0 || nnz < 0)
+    return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused_cmean: bad CMean sizes");
+  const CmeanSpec cm{k_cache, k_rows, page_size, num_kv_heads, loc, nnz};
+  return gqa_impl(q, q_rows, group_size, y, y_rows, head_dim, score, score_rows, aggr, aggr_len, dense_kv_indptr,
+                  sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices, sparse_kv_indices_len,
+                  eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, softmax, scale, &cm, stream);
+}
+
+namespace {
+
+int gqa_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* y, int64_t y_rows,
+             int32_t head_dim, uint16_t* score, int64_t score_rows, uint16_t* aggr, int64_t aggr_len,
+             const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+             int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+             int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
+             int32_t max_num_pages, int32_t softmax, float scale, const CmeanSpec* cms, void* stream) {
   const char* what = "indexer_gqa_fused";
   if (eff_batch_size < 0 || reserved_bos < 0 || reserved_eos < 0)
     return vtx::fail(VTX_E_INVALID, "%s: negative size", what);
@@ -204,6 +331,15 @@ extern "C" int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t 
   if (q_rows < (long long)eff_batch_size * group_size)
     return vtx::fail(VTX_E_INVALID, "%s: %lld query rows for %d segments of %d heads", what, (long long)q_rows,
                      eff_batch_size, group_size);
+  // The CMean runs inside the launch for rows of one 16-byte vector per lane
+  // and decode-sized loc; otherwise as its own launch, first.
+  const bool cm_inside = cms && (head_dim == 64 || head_dim == 128) && cms->nnz <= vtx::kCmLoc;
+  if (cms && !cm_inside && cms->nnz > 0) {
+    const int rc = vtx_page_reduce(cms->k, cms->k_rows, cms->page_size, head_dim, const_cast<uint16_t*>(y),
+                                   VTX_DTYPE_BF16, y_rows, cms->loc, cms->nnz, cms->heads, cms->page_size, 1,
+                                   VTX_REDUCE_MEAN, stream);
+    if (rc != VTX_OK) return rc;
+  }
   if (eff_batch_size == 0) return VTX_OK;
   if (!q || !y || !score || !aggr || !dense_kv_indptr || !sparse_kv_indptr || !dense_kv_indices || !sparse_kv_indices)
     return vtx::fail(VTX_E_INVALID, "%s: null pointer", what);
@@ -241,7 +377,24 @@ extern "C" int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t 
   a.row_cap = (int32_t)cap;
   const size_t lds = (size_t)a.topk * 8 + (size_t)cap * per;
   hipStream_t s = vtx::as_stream(stream);
-  if (max_num_pages <= 256) return launch_g<256>(a, eff_batch_size, lds, s);
-  if (max_num_pages <= 1024) return launch_g<512>(a, eff_batch_size, lds, s);
-  return launch_g<1024>(a, eff_batch_size, lds, s);
+  vtx::CmArgs cma{};
+  const bool cm_launch = cm_inside && cms->nnz > 0;
+  if (cm_launch) {
+    cma.x = cms->k;
+    cma.x_rows = cms->k_rows;
+    cma.rows_per_tile = cms->page_size;
+    cma.cols = head_dim;
+    cma.out = const_cast<uint16_t*>(y);
+    cma.out_rows = y_rows;
+    cma.loc = cms->loc;
+    cma.nnz = cms->nnz;
+    cma.heads = cms->heads;
+    cma.page = cms->page_size;
+  }
+  const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
+  if (max_num_pages <= 256) return launch_g<256>(a, cmp, eff_batch_size, lds, s);
+  if (max_num_pages <= 1024) return launch_g<512>(a, cmp, eff_batch_size, lds, s);
+  return launch_g<1024>(a, cmp, eff_batch_size, lds, s);
 }
+
+}  // namespace

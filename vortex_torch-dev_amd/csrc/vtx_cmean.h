@@ -1,0 +1,152 @@
+// A layer's decode CMean run inside a fused indexer launch (the block-sparse
+// and the GQA indexer kernels): the mean over each closed page's
+// [rows_per_tile, cols] K tile into the centroid pool the launch scores.
+// The tiles are reduced with the page-reduce kernel's own code
+// (vtx_page_reduce.h), and a scored page whose centroid the launch rewrites
+// is scored against the centroid recomputed from its K tile, so the launch
+// writes what a page-reduce launch followed by the indexer would.
+#pragma once
+
+#include "vtx_device.h"
+#include "vtx_page_reduce.h"
+
+namespace vtx {
+
+constexpr int kCmLoc = 256;  // loc entries a launch with an in-kernel CMean scans
+
+struct CmArgs {
+  const uint16_t* x;  // K pool [x_rows, rows_per_tile, cols]
+  int64_t x_rows;
+  int32_t rows_per_tile, cols;
+  uint16_t* out;      // the centroid pool the launch scores
+  int64_t out_rows;
+  const int64_t* loc;
+  int64_t nnz;
+  int32_t heads, page;
+};
+
+// The pages the CMean closes, as one wave holds them (no LDS, no barrier):
+// lane l keeps, for loc entries j * 64 + l (j < kLocRegs), the first tile
+// row (page * H) of the page the entry closes, or -1; mask[j] is the ballot
+// of the closing entries, so "the i-th closed page" is the i-th set bit in
+// loc order, the order the page-reduce kernel lists them in.
+template <int kLocRegs>
+struct Closing {
+  int base[kLocRegs];
+  uint64_t mask[kLocRegs];
+  int count;
+};
+
+// Issues the loads of loc (first in a kernel, so that waiting for them
+// waits for nothing else).
+template <int kLocRegs>
+__device__ __forceinline__ void closing_load(const CmArgs& cm, long long (&pos)[kLocRegs]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    const long long e = (long long)j * kWave + lane;
+    pos[j] = e < cm.nnz ? cm.loc[e] : 0;
+  }
+}
+
+template <int kLocRegs>
+__device__ __forceinline__ Closing<kLocRegs> closing_build(const CmArgs& cm, const long long (&pos)[kLocRegs]) {
+  const int lane = lane_id();
+  Closing<kLocRegs> c;
+  c.count = 0;
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    const long long e = (long long)j * kWave + lane;
+    const bool closes = e < cm.nnz && (pos[j] + 1) % cm.page == 0;  // C semantics, as page-reduce
+    c.base[j] = closes ? (int)((pos[j] / cm.page) * cm.heads) : -1;
+    c.mask[j] = __ballot(closes);
+    c.count += __popcll(c.mask[j]);
+  }
+  return c;
+}
+
+// First tile row of the i-th closed page (i < c.count); wave-uniform i.
+template <int kLocRegs>
+__device__ __forceinline__ int closing_base(const Closing<kLocRegs>& c, int i) {
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    const int n = __popcll(c.mask[j]);
+    if (i < n) {
+      uint64_t m = c.mask[j];
+      for (int k = 0; k < i; ++k) m &= m - 1;
+      return __builtin_amdgcn_readlane(c.base[j], __ffsll((long long)m) - 1);
+    }
+    i -= n;
+  }
+  return -1;
+}
+
+// Tiles first, first + stride, ... of the closed pages (tile t: head t % H
+// of closed page t / H): the mean over each tile's rows into cm.out, exactly
+// as reduce_rows_vec_kernel<LPR, kNeedSum> computes it.  Wave-level.
+template <int LPR, int kLocRegs>
+__device__ __forceinline__ void cmean_tiles(const CmArgs& cm, const Closing<kLocRegs>& c, int first, int stride,
+                                            int grp, int cv) {
+  const int tiles = c.count * cm.heads;
+  for (int t = first; t < tiles; t += stride) {
+    const long long row = (long long)closing_base(c, t / cm.heads) + (t % cm.heads);
+    if (!tile_in_range(cm, row)) continue;
+    Acc acc[8];
+    tile_stats_vec<LPR, kNeedSum>(cm.x, row, cm.rows_per_tile, cm.cols, grp, cv, acc);
+    if (grp == 0) {
+      uint32_t bb[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bb[e] = acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
+      st16(cm.out + row * cm.cols + cv * 8,
+           U4{bb[0] | (bb[1] << 16), bb[2] | (bb[3] << 16), bb[4] | (bb[5] << 16), bb[6] | (bb[7] << 16)});
+    }
+  }
+}
+
+// The centroid of tile row `rid` as the CMean writes it, for the lane's 16-byte
+// column vector: all 64 lanes take part (lane = grp * LPR + col) and every
+// row group ends with the same vector.  Rows of one vector per lane.
+template <int LPR>
+__device__ __forceinline__ U4 fresh_centroid(const CmArgs& cm, int rid, int grp, int col) {
+  Acc acc[8];
+  tile_stats_vec<LPR, kNeedSum>(cm.x, rid, cm.rows_per_tile, cm.cols, grp, col, acc);
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
+  return U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+}
+
+// The score of a query slice (xs: the lane's 8 columns) against a centroid
+// vector: the lane's dot_row chain and the xor tree over the LPR lanes — the
+// bits the scoring pass gives for that row.  Every lane of the row's lane
+// group returns it.
+template <int LPR>
+__device__ __forceinline__ float score_vec(const U4& cen, const float (&xs)[1][8]) {
+  const U4 row[1] = {cen};
+  float f = dot_row<1>(row, xs);
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) f += __shfl_xor(f, d, kWave);
+  return f;
+}
+
+// Whether the lane's pass position (r >= 0, row my_rid) is a tile the
+// in-kernel CMean writes: a row in [page * H, page * H + H) of a closed page,
+// inside the pool and the centroid pool.
+template <int kLocRegs>
+__device__ __forceinline__ bool closes_here(const CmArgs& cm, const Closing<kLocRegs>& c, int r, int my_rid) {
+  const bool cand = r >= 0 && my_rid >= 0 && my_rid < cm.x_rows && my_rid < cm.out_rows;
+  bool fix = false;
+#pragma unroll
+  for (int j = 0; j < kLocRegs; ++j) {
+    uint64_t m = c.mask[j];
+    while (m) {  // wave-uniform
+      const int l = __ffsll((long long)m) - 1;
+      m &= m - 1;
+      const int base = __builtin_amdgcn_readlane(c.base[j], l);
+      fix |= (unsigned)(my_rid - base) < (unsigned)cm.heads;
+    }
+  }
+  return cand && fix;
+}
+
+}  // namespace vtx

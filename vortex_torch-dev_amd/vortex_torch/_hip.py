@@ -72,6 +72,11 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_indexer_gqa_fused_supported": ([_i32, _i32], ctypes.c_int),
+    "vtx_indexer_gqa_fused_cmean": (
+        [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _i64, _i32, _i32, _vp, _i64, _vp],
+        ctypes.c_int,
+    ),
     "vtx_indexer_quest_fused": (
         [_vp, _i64, _i32, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
          _i32, _i32, _i32, _i32, _i32, _vp],
@@ -621,16 +626,21 @@ def indexer_gqa_fused(
     reserved_eos: int,
     max_num_pages: int,
     softmax_scale=None,
+    cmean=None,
 ) -> None:
     """GeMM + segment softmax (unless softmax_scale is None) + max over the
     query heads + topK of one GQA layer in one launch.
 
     q: bf16 [S, G, D]; y: centroid pool [rows, 1, D]; score: the GeMM output
     buffer [pages, 1, G]; aggr: the Max output buffer [pages, 1, 1]; the
-    block tables come from the planner.
+    block tables come from the planner.  cmean: (k_cache [rows, P, D] bf16,
+    loc int64, num_kv_heads) — the layer's page-finish mean into y, run first
+    in the same launch (``vtx_indexer_gqa_fused_cmean``).
     """
     lib = load_library()
     tensors = [q, y, score, aggr, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
+    if cmean is not None:
+        tensors += [cmean[0], cmean[1]]
     dev = _require_gpu(*tensors)
     for t, n in ((q, "q"), (y, "y (centroids)"), (score, "score"), (aggr, "aggr")):
         _req(t, torch.bfloat16, n)
@@ -647,15 +657,26 @@ def indexer_gqa_fused(
     eff = int(eff_batch_size)
     if dense_kv_indptr.numel() < eff + 1 or sparse_kv_indptr.numel() < eff + 1:
         raise RuntimeError(f"vortex_torch: indptr buffers need {eff + 1} entries")
-    with _on_device(dev):
-        rc = lib.vtx_indexer_gqa_fused(
-            q.data_ptr(), S * G, G, y.data_ptr(), y.numel() // D, D,
+    args = (q.data_ptr(), S * G, G, y.data_ptr(), y.numel() // D, D,
             score.data_ptr(), score.numel() // G, aggr.data_ptr(), aggr.numel(),
             dense_kv_indptr.data_ptr(), sparse_kv_indptr.data_ptr(),
             dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
             sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages),
-            0 if softmax_scale is None else 1, float(softmax_scale or 0.0), _stream(dev))
+            0 if softmax_scale is None else 1, float(softmax_scale or 0.0))
+    if cmean is not None:
+        k, loc, heads = cmean
+        _req(k, torch.bfloat16, "k_cache")
+        _req(loc, torch.int64, "loc")
+        if k.dim() != 3 or int(k.shape[2]) != D:
+            raise RuntimeError(f"vortex_torch: CMean pool {tuple(k.shape)} does not match head_dim {D}")
+        with _on_device(dev):
+            rc = lib.vtx_indexer_gqa_fused_cmean(*args, k.data_ptr(), int(k.shape[0]), int(k.shape[1]), int(heads),
+                                                 loc.data_ptr(), loc.numel(), _stream(dev))
+        _check(rc, "indexer_gqa_fused_cmean")
+        return
+    with _on_device(dev):
+        rc = lib.vtx_indexer_gqa_fused(*args, _stream(dev))
     _check(rc, "indexer_gqa_fused")
 
 

@@ -232,12 +232,18 @@ class PendingGemm(_deferred.Pending):
                     break
                 p.flush()
         _deferred.materialize(self.x)
+        # the page-finish mean forward_cache left for these centroids runs in
+        # the same launch (its results, then these)
+        cm = _deferred.take_carry(self.y)
         _hip.indexer_gqa_fused(
             self.x, self.y, self.op.output_buffer, self.max_out,
             ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
             ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
             ctx.page_reserved_eos, ctx.max_num_pages_per_request,
-            softmax_scale=None if self.softmax is None else self.softmax[0])
+            softmax_scale=None if self.softmax is None else self.softmax[0],
+            cmean=None if cm is None else (cm.x, cm.loc, cm.ctx.head_num))
+        if cm is not None:
+            cm.done = True
         self.done = True
 
 
