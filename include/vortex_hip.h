@@ -319,6 +319,28 @@ int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_t group_siz
                             int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                             int32_t reserved_eos, int32_t max_num_pages, void* stream);
 
+/*
+ * vtx_indexer_quest_fused preceded by the layer's CMax + CMin into ymax and
+ * ymin: the results of vtx_page_reduce_multi(k_cache, k_rows, page_size,
+ * head_dim, 2, {ymax, ymin}, {BF16, BF16}, {VTX_REDUCE_MAX, VTX_REDUCE_MIN},
+ * y_rows, loc, nnz, num_kv_heads, page_size, 1) followed by
+ * vtx_indexer_quest_fused with the same arguments, bit for bit (ymax and
+ * ymin are written).  No single counterpart in the reference: the cache
+ * step of gqa_quest_sparse_attention (vortex_torch/flow/algorithms.py:356-496)
+ * and its indexer step in one launch, for head_dim 64 / 128 and nnz <= 256
+ * (otherwise the page reduce is its own launch, first).
+ */
+int vtx_indexer_quest_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                                  uint16_t* ymax, uint16_t* ymin, int64_t y_rows, int32_t head_dim,
+                                  uint16_t* sum, int64_t sum_rows, uint16_t* aggr, int64_t aggr_len,
+                                  const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                                  const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                                  int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                                  int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                                  int32_t reserved_eos, int32_t max_num_pages, const uint16_t* k_cache,
+                                  int64_t k_rows, int32_t page_size, int32_t num_kv_heads,
+                                  const int64_t* loc, int64_t nnz, void* stream);
+
 /* 1 if vtx_indexer_quest_fused handles this head_dim and group size. */
 int vtx_indexer_quest_fused_supported(int32_t head_dim, int32_t group_size);
 

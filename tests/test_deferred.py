@@ -26,7 +26,8 @@ def launches(monkeypatch):
     monkeypatch.setattr(CR, "_recordable_operands", lambda x, out, loc: True)
     monkeypatch.setattr(_hip, "ragged_binary", rec("binary"))
     monkeypatch.setattr(_hip, "ragged_reduce", rec("reduce"))
-    monkeypatch.setattr(_hip, "indexer_quest_fused", rec("fused"))
+    monkeypatch.setattr(_hip, "indexer_quest_fused",
+                        lambda *a, **k: log.append("fused" + ("+envelope" if k.get("envelope") else "")))
     monkeypatch.setattr(_hip, "topk_select", rec("topk"))
     monkeypatch.setattr(_hip, "page_reduce", rec("page_reduce"))
     monkeypatch.setattr(_hip, "page_reduce_multi", lambda x, outs, *a, **k: log.append(f"page_reduce_multi{len(outs)}"))
@@ -108,7 +109,14 @@ def test_quest_chain_broken_by_a_read(launches, monkeypatch):
 
 
 def test_quest_cache_reductions_are_one_pass(launches):
-    """forward_cache's CMax and CMin of the same pool and loc: one launch."""
+    """forward_cache's CMax and CMin of the same pool and loc: one pass,
+    carried into the Quest chain's fused launch."""
+    _run("gqa_quest_sparse_attention", cache_step=True)
+    assert launches == ["fused+envelope"]
+
+
+def test_quest_cache_reductions_one_pass_when_not_carried(launches, monkeypatch):
+    monkeypatch.setenv("VORTEX_FUSE_CMEAN", "0")
     _run("gqa_quest_sparse_attention", cache_step=True)
     assert launches == ["page_reduce_multi2", "fused"]
 
@@ -220,9 +228,17 @@ def test_carried_cmean_for_other_centroids_is_not_consumed(carry_launches):
 
 
 def test_unconsumed_carry_runs_at_indexer_exit(carry_launches):
-    layer = _Layer("gqa_quest_sparse_attention")  # CMax + CMin: one multi pass, not carried
+    name = "test_cmean_no_indexer"
+    if not registry.has(name):
+        @registry.register(name)
+        class _NoIndexer(algorithms.BlockSparseAttention):
+            def forward_indexer(self, q, o, cache, ctx):
+                pass
+    layer = _Layer(name)
     layer.cache_step()
-    assert carry_launches == ["page_reduce_multi"]
+    assert carry_launches == []
+    layer.indexer_step()
+    assert carry_launches == ["page_reduce"]
 
 
 def test_carry_off(carry_launches, monkeypatch):

@@ -508,6 +508,42 @@ def test_gqa_fused_cmean_equals_separate_launches(gpu, name, softmax):
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("name", ["c1", "c2", "eos0", "mid", "d64", "big_loc", "d256", "r3", "r9"])
+def test_quest_fused_envelope_equals_separate_launches(gpu, name):
+    """vtx_indexer_quest_fused_cmean writes what vtx_page_reduce_multi (CMax,
+    CMin) then vtx_indexer_quest_fused write: envelopes, row sums, page
+    maxima, block table."""
+    batch, loc = W.cmean_case(name)
+    loc = loc.to(gpu)
+    ic, _ = W.make_contexts(batch, gpu)
+    from vortex_torch.indexer.utils_sglang import plan_decode
+    b = batch.to(gpu)
+    plan_decode(b.seq_lens, b.req_to_token, b.req_indices, ic)
+    H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+    S, rows, n = batch.batch * H, batch.pool_pages * H, ic.dense_kv_indices.numel()
+    q = W.randn_bf16((S, G, D), 1, gpu)
+    k = W.randn_bf16((rows, P, D), 3, gpu)
+    mx0 = W.randn_bf16((rows, 1, D), 2, gpu, std=0.25)
+    mn0 = W.randn_bf16((rows, 1, D), 4, gpu, std=0.25)
+    out = {}
+    for fused in (False, True):
+        mx, mn = mx0.clone(), mn0.clone()
+        sc = _sentinel((n, G, 1), gpu)
+        ag = _sentinel((n, 1, 1), gpu)
+        sp = ic.sparse_kv_indices.clone()
+        args = (q, mx, mn, sc, ag, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp, S,
+                batch.topk, batch.bos, batch.eos, batch.max_pages_per_request)
+        if fused:
+            _hip.indexer_quest_fused(*args, envelope=(k, loc, H))
+        else:
+            _hip.page_reduce_multi(k, [mx, mn], [_hip.REDUCE_MAX, _hip.REDUCE_MIN], loc, H, P, 1)
+            _hip.indexer_quest_fused(*args)
+        torch.cuda.synchronize()
+        out[fused] = (_bits(mx), _bits(mn), _bits(sc), _bits(ag), _np(sp))
+    for a, b in zip(out[False], out[True]):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_gqa_fused_rejects_bad_arguments(gpu):
     batch = W.c1()
     ic, _ = W.make_contexts(batch, gpu)

@@ -256,7 +256,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       closing = vtx::closing_build(cma, cm_pos);
       n_close = closing.count;
     }
-    vtx::cmean_tiles<LPR, kLocRegs>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
+    vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
                                col);
     if (!active) return;
   }

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   // this launch's CMean: wave w of workgroup b reduces tiles w * grid + b, ...
   if constexpr (cm_on) {
     if (!active) closing = vtx::closing_build(cma, cm_pos);
-    vtx::cmean_tiles<LPR, kLocRegs>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x,
+    vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x,
                                     kWaves * (int)gridDim.x, grp, col);
     if (!active) return;
   }

@@ -13,6 +13,7 @@
 // write when launched one by one: the row sums use the shared Quest pass
 // (vtx_score.h), whose per-lane column order and xor tree are the row-sum
 // kernel's.  The [pages, G, D] products and their maximum are not written.
+#include "vtx_cmean.h"
 #include "vtx_device.h"
 #include "vtx_host.h"
 #include "vtx_score.h"
@@ -38,18 +39,45 @@ struct QuestArgs {
   int32_t segments, G, dim, topk, bos, eos, row_cap;
 };
 
-template <int T, int LPR, int VPL, int kG>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_fused_kernel(QuestArgs a) {
+// Quest score of one envelope (mx, mn: the lane's 16-byte column vector of
+// each) for the lane's query slice: the lane's partial in column order and
+// the xor tree over the LPR lanes, as quest_pass_multi computes it.
+template <int LPR>
+__device__ __forceinline__ float quest_vec(const vtx::U4& mx, const vtx::U4& mn, const float (&xs)[8]) {
+  float a[8], b[8];
+  vtx::unpack8(mx, a);
+  vtx::unpack8(mn, b);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s += vtx::bf16r(fmaxf(xs[e] * a[e], xs[e] * b[e]));
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d, vtx::kWave);
+  return s;
+}
+
+// kCmRegs > 0: the launch also runs the layer's CMax + CMin into the envelope
+// pools (loc: up to 64 * kCmRegs entries, rows of one vector per lane), as
+// the block-sparse fused kernel runs its CMean (vtx_cmean.h).
+template <int T, int LPR, int VPL, int kG, int kCmRegs>
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_fused_kernel(QuestArgs a,
+                                                                                         vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   // Two rows per position: half the GeMM's pass keeps the loads of a pass in
-  // registers.  The pass size does not change the sums (each is the xor tree
-  // of its LPR lanes' partials whatever the slot layout).
-  constexpr int kPass = VPL == 1 ? 32 : 16;
+  // registers (a quarter with the in-launch page reduce, whose code would
+  // otherwise push the pass past 128 registers).  The pass size does not
+  // change the sums (each is the xor tree of its LPR lanes' partials
+  // whatever the slot layout).
+  constexpr int kPass = (VPL == 1 && kCmRegs == 0) ? 32 : 16;
+  constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
+  constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
+  __shared__ int32_t fix_pos[vtx::kCmLoc];  // positions scored after the loop (CMax + CMin)
+  __shared__ int fix_n;
 
   const int seg = blockIdx.x;
+  const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
   const int wave = threadIdx.x / vtx::kWave;
   const int grp = lane / LPR;
@@ -58,22 +86,34 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   const int D = a.dim;
   const int G = a.G;
 
+  long long cm_pos[kLocRegs];
+  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
   const long long start = (long long)a.dindptr[seg] + a.bos;
   const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
   const long long obase = (long long)a.sindptr[seg] + a.bos;
-  if (!(k > 0 && n > k) || start < 0 || start + n > a.sum_rows || start + n > a.aggr_len ||
-      start + n > a.didx_len || obase < 0 || obase + k > a.sidx_len)
-    return;  // uniform: the separate ops write nothing for this segment either
+  const bool active = k > 0 && n > k && start >= 0 && start + n <= a.sum_rows && start + n <= a.aggr_len &&
+                      start + n <= a.didx_len && obase >= 0 && obase + k <= a.sidx_len;
+  if constexpr (!cm_on) {
+    if (!active) return;  // uniform: the separate ops write nothing for this segment either
+  }
   const bool cached = n <= a.row_cap;
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
-  vtx::select_init<T>(sel, k, sh);
-  __syncthreads();  // histogram cleared before any wave counts into it
-
-  // ---- scores, page maxima and keys of every middle page
   const int32_t* dseg = a.didx + start;
   const uint16_t* qs = a.q + (long long)seg * G * D;
+  vtx::Closing<kLocRegs> closing{};
+  int n_close = 0;
+  if (active) {  // uniform
+  vtx::select_init<T>(sel, k, sh);
+  if (cm_on && tid == 0) fix_n = 0;
+  __syncthreads();  // histogram cleared before any wave counts into it
+  if constexpr (cm_on) {
+    closing = vtx::closing_build(cma, cm_pos);
+    n_close = closing.count;
+  }
+
+  // ---- scores, page maxima and keys of every middle page
   long long share = (n + kWaves - 1) / kWaves;
   share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
   if (share > kPass) share = kPass;
@@ -108,6 +148,10 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
       }
     }
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
+    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
+      fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);  // its envelopes are rewritten: scored after the loop
+      r = -1;
+    }
     if (r >= 0) {
       const uint32_t ab = vtx::f32_to_bf16(best);
       const uint32_t key = vtx::score_key(ab);
@@ -119,7 +163,47 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
       vtx::select_count<T>(key, sh);
     }
   }
+  }  // active
+  // this launch's CMax + CMin: wave w of workgroup b reduces tiles w * grid + b, ...
+  if constexpr (cm_on) {
+    if (!active) closing = vtx::closing_build(cma, cm_pos);
+    vtx::cmean_tiles<LPR, kLocRegs, vtx::kEnvelope>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x,
+                                                    kWaves * (int)gridDim.x, grp, col);
+    if (!active) return;
+  }
   __syncthreads();
+
+  // ---- pages whose envelopes this launch rewrites: scored against the
+  // recomputed envelopes, a wave each
+  if constexpr (cm_on) {
+    if (n_close > 0 && fix_n > 0) {  // uniform
+      for (int i = wave; i < fix_n; i += kWaves) {
+        const int pos = fix_pos[i];
+        const int rid = dseg[pos];
+        vtx::U4 emx, emn;
+        vtx::fresh_envelope<LPR>(cma, rid, grp, col, emx, emn);
+        float best = -INFINITY;
+        for (int g = 0; g < G; ++g) {
+          float xg[8];
+          vtx::unpack8(vtx::ld16(qs + (long long)g * D + col * 8), xg);
+          const uint32_t b = vtx::f32_to_bf16(quest_vec<LPR>(emx, emn, xg));
+          if (lane == 0) a.sum[(start + pos) * G + g] = (uint16_t)b;
+          best = fmaxf(best, vtx::bf16_to_f32(b));
+        }
+        if (lane == 0) {
+          const uint32_t ab = vtx::f32_to_bf16(best);
+          const uint32_t key = vtx::score_key(ab);
+          a.aggr[start + pos] = (uint16_t)ab;
+          if (cached) {
+            keys[pos] = (uint16_t)key;
+            rows[pos] = rid;
+          }
+          vtx::select_count<T>(key, sh);
+        }
+      }
+      __syncthreads();
+    }
+  }
 
   // ---- top-k of the segment
   if (cached) {
@@ -136,22 +220,38 @@ constexpr int kMaxTopk = 4096;
 constexpr int kMaxGroup = 8;
 
 template <int T, int kG>
-int launch_dim(const QuestArgs& a, int grid, size_t lds, hipStream_t s) {
+int launch_dim(const QuestArgs& a, const vtx::CmArgs* cm, int grid, size_t lds, hipStream_t s) {
+  const vtx::CmArgs none{};
+  if (cm) {  // the in-kernel CMax + CMin: rows of one 16-byte vector per lane
+    const bool one = cm->nnz <= vtx::kWave;
+    switch (a.dim) {
+      case 64:
+        if (one) quest_fused_kernel<T, 8, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
+        else quest_fused_kernel<T, 8, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        break;
+      case 128:
+        if (one) quest_fused_kernel<T, 16, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
+        else quest_fused_kernel<T, 16, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        break;
+      default: return vtx::fail(VTX_E_INVALID, "indexer_quest_fused: in-kernel page reduce needs head_dim 64 or 128");
+    }
+    return vtx::check_launch("indexer_quest_fused (with CMax + CMin)");
+  }
   switch (a.dim) {
-    case 64: quest_fused_kernel<T, 8, 1, kG><<<grid, T, lds, s>>>(a); break;
-    case 128: quest_fused_kernel<T, 16, 1, kG><<<grid, T, lds, s>>>(a); break;
-    case 256: quest_fused_kernel<(T > 512 ? 512 : T), 16, 2, 1><<<grid, (T > 512 ? 512 : T), lds, s>>>(a); break;
+    case 64: quest_fused_kernel<T, 8, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
+    case 128: quest_fused_kernel<T, 16, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
+    case 256: quest_fused_kernel<(T > 512 ? 512 : T), 16, 2, 1, 0><<<grid, (T > 512 ? 512 : T), lds, s>>>(a, none); break;
     // wide rows keep their query slice in registers: fewer threads, no spills
-    case 512: quest_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1><<<grid, (T > 512 ? 512 : T), lds, s>>>(a); break;
-    case 576: quest_fused_kernel<256, 8, 9, 1><<<grid, 256, lds, s>>>(a); break;
+    case 512: quest_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1, 0><<<grid, (T > 512 ? 512 : T), lds, s>>>(a, none); break;
+    case 576: quest_fused_kernel<256, 8, 9, 1, 0><<<grid, 256, lds, s>>>(a, none); break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_quest_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_quest_fused");
 }
 
 template <int T>
-int launch_g(const QuestArgs& a, int grid, size_t lds, hipStream_t s) {
-  return a.G >= 2 ? launch_dim<T, 2>(a, grid, lds, s) : launch_dim<T, 1>(a, grid, lds, s);
+int launch_g(const QuestArgs& a, const vtx::CmArgs* cm, int grid, size_t lds, hipStream_t s) {
+  return a.G >= 2 ? launch_dim<T, 2>(a, cm, grid, lds, s) : launch_dim<T, 1>(a, cm, grid, lds, s);
 }
 
 }  // namespace
@@ -160,6 +260,26 @@ extern "C" int vtx_indexer_quest_fused_supported(int32_t head_dim, int32_t group
   return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512 || head_dim == 576) &&
          group_size >= 1 && group_size <= kMaxGroup;
 }
+
+namespace {
+
+// The decode CMax + CMin a Quest launch may run first (vtx_indexer_quest_fused_cmean).
+struct CmeanSpec {
+  const uint16_t* k;
+  int64_t k_rows;
+  int32_t page_size, heads;
+  const int64_t* loc;
+  int64_t nnz;
+};
+
+int quest_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* ymax, const uint16_t* ymin,
+               int64_t y_rows, int32_t head_dim, uint16_t* sum, int64_t sum_rows, uint16_t* aggr, int64_t aggr_len,
+               const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+               int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+               int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
+               int32_t max_num_pages, const CmeanSpec* cms, void* stream);
+
+}  // namespace
 
 extern "C" int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                                        const uint16_t* ymax, const uint16_t* ymin, int64_t y_rows,
@@ -171,6 +291,42 @@ extern "C" int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_
                                        int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
                                        void* stream) {
   vtx::clear_error();
+  return quest_impl(q, q_rows, group_size, ymax, ymin, y_rows, head_dim, sum, sum_rows, aggr, aggr_len,
+                    dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
+                    sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
+                    nullptr, stream);
+}
+
+extern "C" int vtx_indexer_quest_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                                             uint16_t* ymax, uint16_t* ymin, int64_t y_rows, int32_t head_dim,
+                                             uint16_t* sum, int64_t sum_rows, uint16_t* aggr, int64_t aggr_len,
+                                             const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                                             const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                                             int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                                             int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                                             int32_t reserved_eos, int32_t max_num_pages, const uint16_t* k_cache,
+                                             int64_t k_rows, int32_t page_size, int32_t num_kv_heads,
+                                             const int64_t* loc, int64_t nnz, void* stream) {
+  vtx::clear_error();
+  if (!k_cache || (nnz > 0 && !loc))
+    return vtx::fail(VTX_E_INVALID, "indexer_quest_fused_cmean: null K pool or loc");
+  if (page_size < 1 || num_kv_heads < 1 || k_rows < 0 || nnz < 0)
+    return vtx::fail(VTX_E_INVALID, "indexer_quest_fused_cmean: bad page-reduce sizes");
+  const CmeanSpec cm{k_cache, k_rows, page_size, num_kv_heads, loc, nnz};
+  return quest_impl(q, q_rows, group_size, ymax, ymin, y_rows, head_dim, sum, sum_rows, aggr, aggr_len,
+                    dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
+                    sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, &cm,
+                    stream);
+}
+
+namespace {
+
+int quest_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16_t* ymax, const uint16_t* ymin,
+               int64_t y_rows, int32_t head_dim, uint16_t* sum, int64_t sum_rows, uint16_t* aggr, int64_t aggr_len,
+               const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
+               int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+               int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
+               int32_t max_num_pages, const CmeanSpec* cms, void* stream) {
   const char* what = "indexer_quest_fused";
   if (eff_batch_size < 0 || reserved_bos < 0 || reserved_eos < 0)
     return vtx::fail(VTX_E_INVALID, "%s: negative size", what);
@@ -181,6 +337,17 @@ extern "C" int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_
   if (q_rows < (long long)eff_batch_size * group_size)
     return vtx::fail(VTX_E_INVALID, "%s: %lld query rows for %d segments of %d heads", what, (long long)q_rows,
                      eff_batch_size, group_size);
+  // CMax + CMin run inside the launch for rows of one 16-byte vector per lane
+  // and decode-sized loc; otherwise as one page-reduce pass of their own, first.
+  const bool cm_inside = cms && (head_dim == 64 || head_dim == 128) && cms->nnz <= vtx::kCmLoc;
+  if (cms && !cm_inside && cms->nnz > 0) {
+    void* const outs[2] = {const_cast<uint16_t*>(ymax), const_cast<uint16_t*>(ymin)};
+    const int32_t dtypes[2] = {VTX_DTYPE_BF16, VTX_DTYPE_BF16};
+    const int32_t types[2] = {VTX_REDUCE_MAX, VTX_REDUCE_MIN};
+    const int rc = vtx_page_reduce_multi(cms->k, cms->k_rows, cms->page_size, head_dim, 2, outs, dtypes, types,
+                                         y_rows, cms->loc, cms->nnz, cms->heads, cms->page_size, 1, stream);
+    if (rc != VTX_OK) return rc;
+  }
   if (eff_batch_size == 0) return VTX_OK;
   if (!q || !ymax || !ymin || !sum || !aggr || !dense_kv_indptr || !sparse_kv_indptr || !dense_kv_indices ||
       !sparse_kv_indices)
@@ -217,7 +384,25 @@ extern "C" int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_
   a.row_cap = (int32_t)cap;
   const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 6;
   hipStream_t s = vtx::as_stream(stream);
-  if (max_num_pages <= 256) return launch_g<256>(a, eff_batch_size, lds, s);
-  if (max_num_pages <= 1024) return launch_g<512>(a, eff_batch_size, lds, s);
-  return launch_g<1024>(a, eff_batch_size, lds, s);
+  vtx::CmArgs cma{};
+  const bool cm_launch = cm_inside && cms->nnz > 0;
+  if (cm_launch) {
+    cma.x = cms->k;
+    cma.x_rows = cms->k_rows;
+    cma.rows_per_tile = cms->page_size;
+    cma.cols = head_dim;
+    cma.out = const_cast<uint16_t*>(ymax);
+    cma.out2 = const_cast<uint16_t*>(ymin);
+    cma.out_rows = y_rows;
+    cma.loc = cms->loc;
+    cma.nnz = cms->nnz;
+    cma.heads = cms->heads;
+    cma.page = cms->page_size;
+  }
+  const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
+  if (max_num_pages <= 256) return launch_g<256>(a, cmp, eff_batch_size, lds, s);
+  if (max_num_pages <= 1024) return launch_g<512>(a, cmp, eff_batch_size, lds, s);
+  return launch_g<1024>(a, cmp, eff_batch_size, lds, s);
 }
+
+}  // namespace

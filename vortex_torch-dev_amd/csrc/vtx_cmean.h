@@ -1,6 +1,7 @@
-// A layer's decode CMean run inside a fused indexer launch (the block-sparse
-// and the GQA indexer kernels): the mean over each closed page's
-// [rows_per_tile, cols] K tile into the centroid pool the launch scores.
+// A layer's decode page reduce run inside a fused indexer launch: the mean
+// over each closed page's [rows_per_tile, cols] K tile into the centroid pool
+// the launch scores (block-sparse and GQA kernels), or its max and min into
+// the envelope pools (Quest kernel).
 // The tiles are reduced with the page-reduce kernel's own code
 // (vtx_page_reduce.h), and a scored page whose centroid the launch rewrites
 // is scored against the centroid recomputed from its K tile, so the launch
@@ -18,12 +19,17 @@ struct CmArgs {
   const uint16_t* x;  // K pool [x_rows, rows_per_tile, cols]
   int64_t x_rows;
   int32_t rows_per_tile, cols;
-  uint16_t* out;      // the centroid pool the launch scores
+  uint16_t* out;      // the centroid pool the launch scores (the max envelope for kEnvelope)
+  uint16_t* out2;     // the min envelope (kEnvelope)
   int64_t out_rows;
   const int64_t* loc;
   int64_t nnz;
   int32_t heads, page;
 };
+
+// What the in-launch page reduce writes: the mean (CMean) or the max and min
+// envelopes (CMax + CMin, as one page_reduce_multi pass writes them).
+enum CmKind { kCentroid = 0, kEnvelope = 1 };
 
 // The pages the CMean closes, as one wave holds them (no LDS, no barrier):
 // lane l keeps, for loc entries j * 64 + l (j < kLocRegs), the first tile
@@ -81,24 +87,36 @@ __device__ __forceinline__ int closing_base(const Closing<kLocRegs>& c, int i) {
   return -1;
 }
 
+__device__ __forceinline__ U4 pack_value(const Acc (&acc)[8], int type, int count) {
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = acc_value(acc[e], type, count);
+  return U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+}
+
 // Tiles first, first + stride, ... of the closed pages (tile t: head t % H
-// of closed page t / H): the mean over each tile's rows into cm.out, exactly
-// as reduce_rows_vec_kernel<LPR, kNeedSum> computes it.  Wave-level.
-template <int LPR, int kLocRegs>
+// of closed page t / H): the mean (kCentroid) or the max and min (kEnvelope)
+// over each tile's rows into cm.out (and cm.out2), exactly as
+// reduce_rows_vec_kernel computes them (max and min are exact, whatever
+// else that kernel accumulates).  Wave-level.
+template <int LPR, int kLocRegs, int kKind>
 __device__ __forceinline__ void cmean_tiles(const CmArgs& cm, const Closing<kLocRegs>& c, int first, int stride,
                                             int grp, int cv) {
+  constexpr int kNeed = kKind == kCentroid ? kNeedSum : (kNeedMax | kNeedMin);
   const int tiles = c.count * cm.heads;
   for (int t = first; t < tiles; t += stride) {
     const long long row = (long long)closing_base(c, t / cm.heads) + (t % cm.heads);
     if (!tile_in_range(cm, row)) continue;
     Acc acc[8];
-    tile_stats_vec<LPR, kNeedSum>(cm.x, row, cm.rows_per_tile, cm.cols, grp, cv, acc);
+    tile_stats_vec<LPR, kNeed>(cm.x, row, cm.rows_per_tile, cm.cols, grp, cv, acc);
     if (grp == 0) {
-      uint32_t bb[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) bb[e] = acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
-      st16(cm.out + row * cm.cols + cv * 8,
-           U4{bb[0] | (bb[1] << 16), bb[2] | (bb[3] << 16), bb[4] | (bb[5] << 16), bb[6] | (bb[7] << 16)});
+      const long long elem = row * cm.cols + cv * 8;
+      if constexpr (kKind == kCentroid) {
+        st16(cm.out + elem, pack_value(acc, VTX_REDUCE_MEAN, cm.rows_per_tile));
+      } else {
+        st16(cm.out + elem, pack_value(acc, VTX_REDUCE_MAX, cm.rows_per_tile));
+        st16(cm.out2 + elem, pack_value(acc, VTX_REDUCE_MIN, cm.rows_per_tile));
+      }
     }
   }
 }
@@ -110,10 +128,17 @@ template <int LPR>
 __device__ __forceinline__ U4 fresh_centroid(const CmArgs& cm, int rid, int grp, int col) {
   Acc acc[8];
   tile_stats_vec<LPR, kNeedSum>(cm.x, rid, cm.rows_per_tile, cm.cols, grp, col, acc);
-  uint32_t b[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) b[e] = acc_value(acc[e], VTX_REDUCE_MEAN, cm.rows_per_tile);
-  return U4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+  return pack_value(acc, VTX_REDUCE_MEAN, cm.rows_per_tile);
+}
+
+// The max and min envelope vectors of tile row `rid`, as CMax and CMin write
+// them (same lane layout as fresh_centroid).
+template <int LPR>
+__device__ __forceinline__ void fresh_envelope(const CmArgs& cm, int rid, int grp, int col, U4& mx, U4& mn) {
+  Acc acc[8];
+  tile_stats_vec<LPR, kNeedMax | kNeedMin>(cm.x, rid, cm.rows_per_tile, cm.cols, grp, col, acc);
+  mx = pack_value(acc, VTX_REDUCE_MAX, cm.rows_per_tile);
+  mn = pack_value(acc, VTX_REDUCE_MIN, cm.rows_per_tile);
 }
 
 // The score of a query slice (xs: the lane's 8 columns) against a centroid

@@ -156,9 +156,9 @@ def current_scope() -> Optional[Scope]:
 
 
 # ---------------------------------------------------------------- the carry
-# forward_cache's page-finish mean may be left unlaunched when the method
-# returns (the *carry*), for the next forward_indexer to run inside its fused
-# launch (vtx_indexer_fused_cmean).  It is launched on its own, on the stream
+# forward_cache's page-finish mean (or CMax + CMin) may be left unlaunched
+# when the method returns (the *carry*), for the next forward_indexer to run
+# inside its fused launch (vtx_indexer_fused_cmean and its GQA / Quest forms).  It is launched on its own, on the stream
 # it was recorded on, as soon as anything else could observe it:
 #   * any other kernel launch of this package (every _hip wrapper checks);
 #   * any torch operation on a layout-tagged tensor (vTensor) that shares
@@ -217,22 +217,46 @@ def carry_touched_by(args, kwargs) -> bool:
     return bool(mine & _storages([args, kwargs or {}], set()))
 
 
-def take_carry(y: torch.Tensor):
-    """The carried page-finish mean if it writes the centroid pool `y` and
-    was recorded on the current stream (the caller then runs it); None
-    otherwise (anything carried is launched first)."""
+def _same(a: torch.Tensor, b: torch.Tensor) -> bool:
+    with torch._C.DisableTorchFunctionSubclass():
+        return a.data_ptr() == b.data_ptr() and a.shape == b.shape
+
+
+def _take_if(ok) -> Optional[Pending]:
     c = current_carry()
     if c is None:
         return None
     pending, stream = c
-    with torch._C.DisableTorchFunctionSubclass():
-        same = (pending.outs[0].data_ptr() == y.data_ptr() and pending.outs[0].shape == y.shape
-                and _stream_of(y.device) == stream)
-    if not same:
+    if not ok(pending) or _stream_of(pending.x.device) != stream:
         flush_carry()
         return None
     _tls.carry = None
     return pending
+
+
+def take_carry(y: torch.Tensor):
+    """The carried page-finish mean if it writes the centroid pool `y` and
+    was recorded on the current stream (the caller then runs it); None
+    otherwise (anything carried is launched first)."""
+    return _take_if(lambda p: p.carry_kind() == "mean" and _same(p.outs[0], y))
+
+
+def take_carry_envelope(ya: torch.Tensor, yb: torch.Tensor):
+    """The carried CMax + CMin if their outputs are the pools ya and yb (in
+    either role), as (record, max pool, min pool); None otherwise (anything
+    carried is launched first)."""
+    from . import _hip
+
+    def ok(p):
+        if p.carry_kind() != "envelope":
+            return False
+        mx, mn = p.output_of(_hip.REDUCE_MAX), p.output_of(_hip.REDUCE_MIN)
+        return (_same(mx, ya) and _same(mn, yb)) or (_same(mx, yb) and _same(mn, ya))
+
+    p = _take_if(ok)
+    if p is None:
+        return None
+    return p, p.output_of(_hip.REDUCE_MAX), p.output_of(_hip.REDUCE_MIN)
 
 
 @contextlib.contextmanager

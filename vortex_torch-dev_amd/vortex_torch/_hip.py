@@ -83,6 +83,11 @@ _SIGNATURES = {
         ctypes.c_int,
     ),
     "vtx_indexer_quest_fused_supported": ([_i32, _i32], ctypes.c_int),
+    "vtx_indexer_quest_fused_cmean": (
+        [_vp, _i64, _i32, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _vp],
+        ctypes.c_int,
+    ),
     "vtx_ragged_gemm": (
         [_vp, _i64, _i32, _i32, _vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64,
          _vp, _vp],
@@ -700,9 +705,12 @@ def indexer_quest_fused(
     reserved_bos: int,
     reserved_eos: int,
     max_num_pages: int,
+    envelope=None,
 ) -> None:
     """Quest envelope scores + max over the query heads + topK of one layer
-    in one launch.
+    in one launch.  envelope: (k_cache [rows, P, D] bf16, loc int64,
+    num_kv_heads) — the layer's CMax into ymax and CMin into ymin, run first in
+    the same launch (``vtx_indexer_quest_fused_cmean``).
 
     q: bf16 [S, G, D]; ymax, ymin: the envelope pools [rows, 1, D]; score:
     the Sum(dim=2) output buffer [pages, G, 1]; aggr: the Max(dim=1) output
@@ -728,14 +736,26 @@ def indexer_quest_fused(
     eff = int(eff_batch_size)
     if dense_kv_indptr.numel() < eff + 1 or sparse_kv_indptr.numel() < eff + 1:
         raise RuntimeError(f"vortex_torch: indptr buffers need {eff + 1} entries")
-    with _on_device(dev):
-        rc = lib.vtx_indexer_quest_fused(
-            q.data_ptr(), S * G, G, ymax.data_ptr(), ymin.data_ptr(), ymax.numel() // D, D,
+    args = (q.data_ptr(), S * G, G, ymax.data_ptr(), ymin.data_ptr(), ymax.numel() // D, D,
             score.data_ptr(), score.numel() // G, aggr.data_ptr(), aggr.numel(),
             dense_kv_indptr.data_ptr(), sparse_kv_indptr.data_ptr(),
             dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
             sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
-            eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), _stream(dev))
+            eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages))
+    if envelope is not None:
+        k, loc, heads = envelope
+        _require_gpu(k, loc)
+        _req(k, torch.bfloat16, "k_cache")
+        _req(loc, torch.int64, "loc")
+        if k.dim() != 3 or int(k.shape[2]) != D:
+            raise RuntimeError(f"vortex_torch: envelope pool {tuple(k.shape)} does not match head_dim {D}")
+        with _on_device(dev):
+            rc = lib.vtx_indexer_quest_fused_cmean(*args, k.data_ptr(), int(k.shape[0]), int(k.shape[1]),
+                                                   int(heads), loc.data_ptr(), loc.numel(), _stream(dev))
+        _check(rc, "indexer_quest_fused_cmean")
+        return
+    with _on_device(dev):
+        rc = lib.vtx_indexer_quest_fused(*args, _stream(dev))
     _check(rc, "indexer_quest_fused")
 
 

@@ -77,19 +77,36 @@ class _PendingPageReduce(_deferred.Pending):
     #: loc entries the fused indexer launch scans for a carried mean
     CARRY_MAX_LOC = 256
 
+    def carry_kind(self):
+        """"mean" (one CMean) or "envelope" (a CMax and a CMin), the page
+        reduces a fused indexer launch can run; None for anything else."""
+        kinds = sorted(self.types)
+        if kinds == [_hip.REDUCE_MEAN]:
+            return "mean"
+        if kinds == sorted([_hip.REDUCE_MAX, _hip.REDUCE_MIN]):
+            return "envelope"
+        return None
+
+    def output_of(self, kernel_type: int) -> torch.Tensor:
+        return self.outs[self.types.index(kernel_type)]
+
     def carryable(self) -> bool:
         """Whether the next forward_indexer's fused launch may run this record
-        (vtx_indexer_fused_cmean): a single decode-sized mean (dim 1) of
-        [page_size, D] tiles into a bf16 [rows, 1, D] centroid pool."""
-        if self.done or len(self.outs) != 1 or self.types[0] != _hip.REDUCE_MEAN or self.dim != 1:
+        (vtx_indexer_fused_cmean and its GQA / Quest forms): a decode-sized
+        CMean, or CMax + CMin, (dim 1) of [page_size, D] tiles into bf16
+        [rows, 1, D] pools."""
+        if self.done or self.dim != 1 or self.carry_kind() is None:
             return False
-        out, x = self.outs[0], self.x
-        if not _recordable_operands(x, out, self.loc):
-            return False
+        x = self.x
+        for out in self.outs:
+            if not _recordable_operands(x, out, self.loc):
+                return False
+            with torch._C.DisableTorchFunctionSubclass():
+                if not (out.dtype == torch.bfloat16 and out.dim() == 3 and x.dim() == 3 and int(out.shape[1]) == 1
+                        and int(x.shape[2]) == int(out.shape[2])):
+                    return False
         with torch._C.DisableTorchFunctionSubclass():
-            return (out.dtype == torch.bfloat16 and out.dim() == 3 and x.dim() == 3
-                    and int(out.shape[1]) == 1 and int(x.shape[2]) == int(out.shape[2])
-                    and int(x.shape[1]) == int(self.ctx.page_size) and self.loc.numel() <= self.CARRY_MAX_LOC)
+            return int(x.shape[1]) == int(self.ctx.page_size) and self.loc.numel() <= self.CARRY_MAX_LOC
 
     def _run(self) -> None:
         c = self.ctx

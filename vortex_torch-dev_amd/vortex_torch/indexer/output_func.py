@@ -112,11 +112,20 @@ def _fuse_quest(chain, o: torch.Tensor, ctx: Context) -> None:
             p.flush()
     for d in pa.deps + pb.deps:  # recorded producers of q and the envelopes
         d.flush()
+    # the CMax + CMin forward_cache left for these envelopes run in the same
+    # launch (their results, then these); the score is symmetric in the two
+    ya, yb = pa.info["y"], pb.info["y"]
+    env = _deferred.take_carry_envelope(ya, yb)
+    if env is not None:
+        ya, yb = env[1], env[2]
     _hip.indexer_quest_fused(
-        pa.info["x"], pa.info["y"], pb.info["y"], rsum.info["out"], aggr.info["out"],
+        pa.info["x"], ya, yb, rsum.info["out"], aggr.info["out"],
         ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
         ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
-        ctx.page_reserved_eos, ctx.max_num_pages_per_request)
+        ctx.page_reserved_eos, ctx.max_num_pages_per_request,
+        envelope=None if env is None else (env[0].x, env[0].loc, env[0].ctx.head_num))
+    if env is not None:
+        env[0].done = True
     rsum.done = aggr.done = True
     for p in (pa, pb, mx):
         p.elided = True
