@@ -213,8 +213,8 @@ int vtx_indexer_fused_supported(int32_t head_dim);
  * (cache/triton_kernels/reduce_impl.py:7-89, the cache step of
  * block_sparse_attention, vortex_torch/flow/algorithms.py:20-235) and the
  * layer's indexer step in one launch.  For head_dim 64 / 128, nnz <= 256 and
- * the one-workgroup-per-segment layout the mean runs in extra workgroups of
- * the same launch, and a scored page whose centroid it rewrites is scored
+ * the one-workgroup-per-segment layout the mean's tiles are spread over the
+ * launch's own waves, and a scored page whose centroid it rewrites is scored
  * against the fresh centroid; otherwise it is its own launch, first.
  * k_cache: bf16 [k_rows, page_size, head_dim] with row = page * H + h.
  */

@@ -233,8 +233,11 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
       if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
         // the in-kernel CMean rewrites this page's centroid: scored after the loop
-        fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);
-        r = -1;
+        const int slot = atomicAdd(&fix_n, 1);
+        if (slot < vtx::kCmLoc) {  // (always, unless the segment lists a page twice)
+          fix_pos[slot] = (int32_t)(p0 + r);
+          r = -1;
+        }
       }
       if (r >= 0) {
         const uint32_t sb = vtx::f32_to_bf16(sc);
@@ -267,7 +270,8 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   if constexpr (cm_on) {
     if (n_close > 0 && fix_n > 0) {  // uniform
       if (!have_mean) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-      for (int i = wave; i < fix_n; i += kWaves) {
+      const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
+      for (int i = wave; i < fixes; i += kWaves) {
         const int pos = fix_pos[i];
         const int rid = dseg[pos];
         const float f = vtx::score_vec<LPR>(vtx::fresh_centroid<LPR>(cma, rid, grp, col), xs);

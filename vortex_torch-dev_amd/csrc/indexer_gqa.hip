@@ -138,8 +138,10 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     }
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
     if (cached && r >= 0) rows[p0 + r] = my_rid;
-    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid))
-      fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);  // its scores are redone after the loop
+    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
+      const int slot = atomicAdd(&fix_n, 1);  // its scores are redone after the loop
+      if (slot < vtx::kCmLoc) fix_pos[slot] = (int32_t)(p0 + r);  // (always, unless a page is listed twice)
+    }
   }
   }  // active
   // this launch's CMean: wave w of workgroup b reduces tiles w * grid + b, ...
@@ -155,7 +157,8 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   // against the recomputed centroid, a wave each
   if constexpr (cm_on) {
     if (n_close > 0 && fix_n > 0) {  // uniform
-      for (int i = wave; i < fix_n; i += kWaves) {
+      const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
+      for (int i = wave; i < fixes; i += kWaves) {
         const int pos = fix_pos[i];
         const vtx::U4 cen = vtx::fresh_centroid<LPR>(cma, dseg[pos], grp, col);
         for (int g = 0; g < G; ++g) {

@@ -149,8 +149,11 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
     }
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
     if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
-      fix_pos[atomicAdd(&fix_n, 1)] = (int32_t)(p0 + r);  // its envelopes are rewritten: scored after the loop
-      r = -1;
+      const int slot = atomicAdd(&fix_n, 1);
+      if (slot < vtx::kCmLoc) {  // its envelopes are rewritten: scored after the loop
+        fix_pos[slot] = (int32_t)(p0 + r);  // (always, unless a page is listed twice)
+        r = -1;
+      }
     }
     if (r >= 0) {
       const uint32_t ab = vtx::f32_to_bf16(best);
@@ -177,7 +180,8 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   // recomputed envelopes, a wave each
   if constexpr (cm_on) {
     if (n_close > 0 && fix_n > 0) {  // uniform
-      for (int i = wave; i < fix_n; i += kWaves) {
+      const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
+      for (int i = wave; i < fixes; i += kWaves) {
         const int pos = fix_pos[i];
         const int rid = dseg[pos];
         vtx::U4 emx, emn;
