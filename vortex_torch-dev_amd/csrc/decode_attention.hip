@@ -10,20 +10,23 @@
 // with fp32 scores, an fp32 online softmax and fp32 accumulation.  A segment
 // with no tokens writes zeros.
 //
-// One workgroup (4 waves) per segment.  A wave takes every fourth group of
-// kRowsPerLoad consecutive tokens (LPR lanes per token, 16-byte vectors of
-// K and V), kB groups per batch with all their K and V loads issued before
-// any arithmetic, and keeps a running max and per-lane partial sums; the
-// waves' (max, sum, accumulator) are merged in LDS.  At decode batch sizes
-// the q . K products are G rows against a few hundred tokens: HBM-bound, so
-// the kernel runs on the VALU.
+// One workgroup per segment (8 waves, or 4 for wide G x D).  The segment's
+// page rows are staged in LDS first (one load per page, up to kPageCap
+// pages; longer segments read them from the table), so each batch of a
+// wave costs one memory round trip: a wave takes every kWaves-th group of
+// kRowsPerLoad consecutive tokens (LPR lanes per token, 16-byte vectors of K
+// and V), kB groups per batch, and issues the next batch's K and V loads
+// before it computes on the current one (two register buffers).  It keeps a
+// running max and per-lane partial sums (online softmax); the waves'
+// (max, sum, accumulator) are merged in LDS.  At decode batch sizes the
+// q . K products are G rows against a few hundred tokens: HBM-bound, so the
+// kernel runs on the VALU.
 #include "vtx_device.h"
 #include "vtx_host.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / vtx::kWave;
+constexpr int kPageCap = 2048;  // page rows staged in LDS
 
 struct AttnArgs {
   const uint16_t* q;
@@ -39,10 +42,27 @@ struct AttnArgs {
   float scale;
 };
 
+// Threads per workgroup: 8 waves where a wave's registers fit 128 (rows of
+// one 16-byte vector per lane, at most two query heads), else 4.
 template <int LPR, int VPL, int kG>
-__global__ __launch_bounds__(kThreads) void paged_decode_attention_kernel(AttnArgs a) {
+constexpr int attn_threads() {
+  return VPL == 1 && kG <= 2 ? 512 : 256;
+}
+// Token groups per batch (two batches in registers at a time).
+template <int VPL, int kG>
+constexpr int attn_batch() {
+  return VPL == 1 ? (kG == 1 ? 4 : (kG == 2 ? 3 : 2)) : (kG == 1 ? 2 : 1);
+}
+
+// With 8 waves, at most 128 registers (four waves per SIMD: two workgroups per CU).
+template <int LPR, int VPL, int kG>
+__global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
+                             (attn_threads<LPR, VPL, kG>() == 512 ? 4 : 1)) void paged_decode_attention_kernel(AttnArgs a) {
+  constexpr int T = attn_threads<LPR, VPL, kG>();
+  constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;  // tokens per wave-wide load
-  constexpr int kB = VPL == 1 ? 8 : 4;             // token groups per batch
+  constexpr int kB = attn_batch<VPL, kG>();        // token groups per batch
+  __shared__ int32_t s_rows[kPageCap];
   __shared__ float s_m[kWaves][kG];
   __shared__ float s_l[kWaves][kG];
   __shared__ float s_acc[kWaves][kG][LPR * VPL * 8];
@@ -57,11 +77,20 @@ __global__ __launch_bounds__(kThreads) void paged_decode_attention_kernel(AttnAr
 
   const long long start = a.indptr[seg];
   const long long m = (long long)a.indptr[seg + 1] - start;
-  long long T = 0;  // tokens of the segment
-  if (m > 0 && start >= 0 && start + m <= a.indices_len) {
+  int T_tok = 0;  // tokens of the segment
+  if (m > 0 && start >= 0 && start + m <= a.indices_len && a.rows > 0) {
     int last = a.last_len[seg];
     last = last < 0 ? 0 : (last > P ? P : last);
-    T = (m - 1) * P + last;
+    const long long t = (m - 1) * P + last;
+    T_tok = t < (1LL << 30) ? (int)t : 0;  // (token indices, with the prefetch past the end, fit an int)
+  }
+  // the segment's page rows (-1: outside the pool)
+  const bool staged = m <= kPageCap;
+  if (staged && T_tok > 0) {
+    for (int i = tid; i < (int)m; i += T) {
+      const int r = a.indices[start + i];
+      s_rows[i] = (r >= 0 && r < a.rows) ? r : -1;
+    }
   }
 
   // query slice of this lane (columns (v * LPR + col) * 8 .. + 8)
@@ -88,37 +117,39 @@ __global__ __launch_bounds__(kThreads) void paged_decode_attention_kernel(AttnAr
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][v][e] = 0.f;
   }
+  __syncthreads();  // page rows staged
 
-  const long long groups = (T + kRowsPerLoad - 1) / kRowsPerLoad;
-  for (long long g0 = wave; g0 < groups; g0 += (long long)kWaves * kB) {
-    vtx::U4 kv[kB][VPL], vv[kB][VPL];
-    bool ok[kB];
+  const int groups = (T_tok + kRowsPerLoad - 1) / kRowsPerLoad;
+  // batches of this wave: groups wave + kWaves * (j * kB + i), i < kB
+  const int nb = groups > wave ? (groups - wave + kWaves * kB - 1) / (kWaves * kB) : 0;
+
+  // K and V of batch j; tokens past the segment or on rows outside the pool
+  // load the pool's first row (a valid address) and are masked off
+  auto load = [&](int j, vtx::U4 (&kv)[kB][VPL], vtx::U4 (&vv)[kB][VPL], bool (&ok)[kB]) {
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
-      const long long t = (g0 + (long long)i * kWaves) * kRowsPerLoad + grp;
-      ok[i] = t < T;
-      long long row = 0;
-      int slot = 0;
-      if (ok[i]) {
-        row = a.indices[start + t / P];
-        slot = (int)(t % P);
-        if (row < 0 || row >= a.rows) {
-          ok[i] = false;
-          row = 0;
+      const int t = (wave + kWaves * (j * kB + i)) * kRowsPerLoad + grp;
+      int row = -1, slot = 0;
+      if (t < T_tok) {
+        const int pg = t / P;
+        slot = t - pg * P;
+        if (staged) {
+          row = s_rows[pg];
+        } else {
+          const int r = a.indices[start + pg];
+          row = (r >= 0 && r < a.rows) ? r : -1;
         }
       }
-      const long long base = (row * P + slot) * (long long)D;
+      ok[i] = row >= 0;
+      const long long base = ok[i] ? ((long long)row * P + slot) * (long long)D : 0;
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
-        if (ok[i]) {
-          kv[i][v] = vtx::ld16_stream(a.k + base + (v * LPR + col) * 8);
-          vv[i][v] = vtx::ld16_stream(a.v + base + (v * LPR + col) * 8);
-        } else {
-          kv[i][v] = vtx::U4{0u, 0u, 0u, 0u};
-          vv[i][v] = vtx::U4{0u, 0u, 0u, 0u};
-        }
+        kv[i][v] = vtx::ld16_stream(a.k + base + (v * LPR + col) * 8);
+        vv[i][v] = vtx::ld16_stream(a.v + base + (v * LPR + col) * 8);
       }
     }
+  };
+  auto compute = [&](const vtx::U4 (&kv)[kB][VPL], const vtx::U4 (&vv)[kB][VPL], const bool (&ok)[kB]) {
     // scores: every lane of a token's LPR group ends with the full dot
     float sc[kB][kG];
 #pragma unroll
@@ -159,7 +190,23 @@ __global__ __launch_bounds__(kThreads) void paged_decode_attention_kernel(AttnAr
       }
       mx[g] = nm;
     }
+  };
+
+  // two register buffers: batch j + 1's loads are in flight while batch j
+  // is computed (the loads are unconditional, so the wait for a buffer is
+  // for its own loads only)
+  if (nb > 0) {  // uniform over the wave
+    vtx::U4 ka[kB][VPL], va[kB][VPL], kb[kB][VPL], vb[kB][VPL];
+    bool oka[kB], okb[kB];
+    load(0, ka, va, oka);
+    for (int j = 0; j < nb; j += 2) {
+      load(j + 1, kb, vb, okb);
+      compute(ka, va, oka);
+      load(j + 2, ka, va, oka);
+      if (j + 1 < nb) compute(kb, vb, okb);
+    }
   }
+
   // fold the token groups of the wave (lanes that share col), then the waves
 #pragma unroll
   for (int g = 0; g < kG; ++g) {
@@ -183,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_attention_kernel(AttnAr
   }
   __syncthreads();
   // one thread per (g, column) writes the merged output
-  for (int idx = tid; idx < G * D; idx += kThreads) {
+  for (int idx = tid; idx < G * D; idx += T) {
     const int g = idx / D;
     const int d = idx - g * D;
     float M = -INFINITY;
@@ -202,12 +249,17 @@ __global__ __launch_bounds__(kThreads) void paged_decode_attention_kernel(AttnAr
   }
 }
 
+template <int LPR, int VPL, int kG>
+void launch_one(const AttnArgs& a, hipStream_t s) {
+  paged_decode_attention_kernel<LPR, VPL, kG><<<a.segments, attn_threads<LPR, VPL, kG>(), 0, s>>>(a);
+}
+
 template <int LPR, int VPL>
 int launch_g(const AttnArgs& a, hipStream_t s) {
-  if (a.G <= 1) paged_decode_attention_kernel<LPR, VPL, 1><<<a.segments, kThreads, 0, s>>>(a);
-  else if (a.G <= 2) paged_decode_attention_kernel<LPR, VPL, 2><<<a.segments, kThreads, 0, s>>>(a);
-  else if (a.G <= 4) paged_decode_attention_kernel<LPR, VPL, 4><<<a.segments, kThreads, 0, s>>>(a);
-  else paged_decode_attention_kernel<LPR, VPL, 8><<<a.segments, kThreads, 0, s>>>(a);
+  if (a.G <= 1) launch_one<LPR, VPL, 1>(a, s);
+  else if (a.G <= 2) launch_one<LPR, VPL, 2>(a, s);
+  else if (a.G <= 4) launch_one<LPR, VPL, 4>(a, s);
+  else launch_one<LPR, VPL, 8>(a, s);
   return vtx::check_launch("paged_decode_attention");
 }
 
