@@ -705,6 +705,25 @@ def test_decode_attention_head_shapes(gpu, D, G):
     np.testing.assert_allclose(_f(_bits(o)), _f(exp), rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("G", [1, 2, 4])
+def test_decode_attention_long_segment(gpu, G):
+    """Segments of more pages than the kernel stages in LDS (2048) read their
+    page rows from the table; a short and an empty request beside them."""
+    from vortex_torch.decode_attention import dense_decode_attention
+    from vortex_torch.indexer.utils_sglang import plan_decode
+
+    batch = W.make_batch([33600, 700, 0], pool_pages=2600, seed=31, num_kv_heads=2)
+    ic, _ = W.make_contexts(batch, gpu)
+    b = batch.to(gpu)
+    plan_decode(b.seq_lens, b.req_to_token, b.req_indices, ic)
+    assert int(ic.dense_kv_indptr[1]) - int(ic.dense_kv_indptr[0]) > 2048
+    q, k, v = _attn_inputs(batch, gpu, G, 128, 11)
+    o = dense_decode_attention(q, k, v, ic)
+    exp = O.paged_decode_attention(_bits(q), _bits(k), _bits(v), _np(ic.dense_kv_indptr), _np(ic.dense_kv_indices),
+                                   _np(ic.kv_last_page_len), batch.batch, batch.num_kv_heads, 1.0 / np.sqrt(128))
+    np.testing.assert_allclose(_f(_bits(o)), _f(exp), rtol=1e-2, atol=1e-3)
+
+
 def test_sparse_attention_equals_dense_when_budget_covers_all(gpu):
     """With a budget no smaller than any request, the sparse table is the
     dense one and so is the attention, bit for bit."""
