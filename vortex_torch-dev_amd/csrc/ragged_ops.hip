@@ -82,9 +82,10 @@ using vtx::bf16r;
 // ------------------------------------------------------------------ GeMM
 // o[p, c, g] = bf16(fp32 sum_k x[rx, g, k] * y[ry, c, k]); o is
 // [out_rows, C = y.d0, G = x.d0], K = x.d1 = y.d1 (a multiple of 8).
-// LPR lanes share a position (each one K/8/LPR 16-byte vectors: one fp32
-// multiply-add chain in increasing k), the LPR partial sums are combined by
-// an xor tree; kG query rows are scored per pass over y's row.
+// LPR lanes share a position (each one K/8/LPR 16-byte vectors: one chain
+// of two-product steps, vtx::dot2_bf16, in increasing k), the LPR partial
+// sums are combined by an xor tree; kG query rows are scored per pass over
+// y's row.
 struct GemmArgs {
   Walk w;
   Opnd x, y;
@@ -120,16 +121,15 @@ __global__ __launch_bounds__(kThreads) void gemm_ragged_kernel(GemmArgs a) {
           for (int gg = 0; gg < kG; ++gg) acc[gg] = 0.f;
           for (int v = col; v < units; v += LPR) {
             const vtx::U4 yv = vtx::ld16(yr + v * 8);
-            float yf[8];
-            vtx::unpack8(yv, yf);
 #pragma unroll
             for (int gg = 0; gg < kG; ++gg) {
               if (g0 + gg < G) {
                 const vtx::U4 xv = vtx::ld16(a.x.p + ((ok ? rx : 0) * G + g0 + gg) * (long long)K + v * 8);
-                float xf[8];
-                vtx::unpack8(xv, xf);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[gg] = fmaf(yf[e], xf[e], acc[gg]);
+                // the four two-product steps of vtx::dot_row, in its order
+                acc[gg] = vtx::dot2_bf16(yv.x, xv.x, acc[gg]);
+                acc[gg] = vtx::dot2_bf16(yv.y, xv.y, acc[gg]);
+                acc[gg] = vtx::dot2_bf16(yv.z, xv.z, acc[gg]);
+                acc[gg] = vtx::dot2_bf16(yv.w, xv.w, acc[gg]);
               }
             }
           }

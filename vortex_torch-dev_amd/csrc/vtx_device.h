@@ -124,22 +124,32 @@ __device__ __forceinline__ void unpack8(const U4& t, float* f) {
   f[7] = bf16_hi(t.w);
 }
 
+// Two bf16 products added to an fp32 sum by gfx950's v_dot2c_f32_bf16:
+// c + lo(a) * lo(b) + hi(a) * hi(b), a and b each two packed bf16 values.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// The bf16 bits of two fp32 values that are bf16 values (exact).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+}
+
 // This lane's share of a row dot product: VPL vectors of 8 bf16 against the
-// fp32 query slice, one fused multiply-add chain in column order.  Every
-// scoring kernel uses it, so their scores agree bit for bit.
+// fp32 query slice, whose values are bf16 values (the callers' queries are
+// bf16 rows or bf16-rounded means), as a chain of four two-product steps
+// (dot2_bf16) per vector in column order.  Every scoring kernel uses it, so
+// their scores agree bit for bit.
 template <int VPL>
 __device__ __forceinline__ float dot_row(const U4 (&w)[VPL], const float (&xs)[VPL][8]) {
   float s = 0.f;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
-    s = fmaf(bf16_lo(w[v].x), xs[v][0], s);
-    s = fmaf(bf16_hi(w[v].x), xs[v][1], s);
-    s = fmaf(bf16_lo(w[v].y), xs[v][2], s);
-    s = fmaf(bf16_hi(w[v].y), xs[v][3], s);
-    s = fmaf(bf16_lo(w[v].z), xs[v][4], s);
-    s = fmaf(bf16_hi(w[v].z), xs[v][5], s);
-    s = fmaf(bf16_lo(w[v].w), xs[v][6], s);
-    s = fmaf(bf16_hi(w[v].w), xs[v][7], s);
+    s = dot2_bf16(w[v].x, pack_bf16x2(xs[v][0], xs[v][1]), s);
+    s = dot2_bf16(w[v].y, pack_bf16x2(xs[v][2], xs[v][3]), s);
+    s = dot2_bf16(w[v].z, pack_bf16x2(xs[v][4], xs[v][5]), s);
+    s = dot2_bf16(w[v].w, pack_bf16x2(xs[v][6], xs[v][7]), s);
   }
   return s;
 }
