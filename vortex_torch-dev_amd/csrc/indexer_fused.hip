@@ -69,10 +69,14 @@ struct FusedArgs {
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
 // fp32 mean of its G rows (torch's mean), or the row itself when G == 0.
 // Lanes with `store` set (one lane group per row) also write the mean to x_out.
-template <int LPR, int VPL, int kQRegs>
+// The rows come from qv when q_in_regs (G <= kQRegs; G == 0: the row in
+// qv[0]), else from qb; kRegsOnly: callers that only get here with them in
+// qv (the scoring loop), so no address into q stays live across it.
+template <int LPR, int VPL, int kQRegs, bool kRegsOnly = false>
 __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv)[kQRegs][VPL],
                                           bool q_in_regs, const uint16_t* qb, int seg, bool store,
                                           int col, float (&xs)[VPL][8]) {
+  if constexpr (kRegsOnly) q_in_regs = true;
   const int D = a.dim;
   if (a.G > 0) {
 #pragma unroll
@@ -120,7 +124,7 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
   } else {
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
-      const vtx::U4 t = vtx::ld16(qb + (v * LPR + col) * 8);
+      const vtx::U4 t = q_in_regs ? qv[0][v] : vtx::ld16(qb + (v * LPR + col) * 8);
       xs[v][0] = vtx::bf16_lo(t.x);
       xs[v][1] = vtx::bf16_hi(t.x);
       xs[v][2] = vtx::bf16_lo(t.y);
@@ -163,16 +167,18 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   long long cm_pos[kLocRegs];
   if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
 
-  // ---- 1. query rows (issued first: only needed once centroid rows arrive)
+  // ---- 1. query rows (issued first: only needed once centroid rows arrive;
+  // G == 0: the averaged row itself, in qv[0])
   vtx::U4 qv[kQRegs][VPL];
-  const bool q_in_regs = a.G > 0 && a.G <= kQRegs;
+  const bool q_in_regs = a.G <= kQRegs;
+  const int q_rows_in = a.G > 0 ? a.G : 1;
   const uint16_t* qb = a.G > 0 ? a.q + (long long)seg * a.G * D : a.x + (long long)seg * D;
   if (q_in_regs) {
 #pragma unroll
     for (int g = 0; g < kQRegs; ++g)
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
-        qv[g][v] = g < a.G ? vtx::ld16(qb + (long long)g * D + (v * LPR + col) * 8) : vtx::U4{0u, 0u, 0u, 0u};
+        qv[g][v] = g < q_rows_in ? vtx::ld16(qb + (long long)g * D + (v * LPR + col) * 8) : vtx::U4{0u, 0u, 0u, 0u};
   }
 
   // ---- 2. segment bounds
@@ -205,13 +211,18 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int32_t* dseg = a.didx + start;
   long long share = 0;
   bool have_mean = false;
+  if constexpr (cm_on) {  // the closed pages (loc arrived with the bounds; loc dies here)
+    closing = vtx::closing_build(cma, cm_pos);
+    n_close = closing.count;
+  }
   if (active) {  // uniform
     vtx::select_init<T>(sel, k, sh);
     if (cm_on && tid == 0) fix_n = 0;
     __syncthreads();  // histogram cleared before any wave counts into it
-    if constexpr (cm_on) {
-      closing = vtx::closing_build(cma, cm_pos);
-      n_close = closing.count;
+
+    if (!q_in_regs) {  // (more than kQRegs rows to average: before the loop)
+      query_row<LPR, VPL, kQRegs>(a, qv, false, qb, seg, store_mean, col, xs);
+      have_mean = true;
     }
 
     // ---- 4. scores: the pages are split evenly over the waves (one pass
@@ -225,7 +236,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
       // one coalesced load of the pass's row ids (lane l holds position l)
       const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
       if (!have_mean) {
-        query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+        query_row<LPR, VPL, kQRegs, true>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
         have_mean = true;
       }
       int r;
@@ -255,10 +266,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // + waves * grid, ... (one tile per wave 0 for up to `grid` tiles), after
   // its passes (the registers of the scoring loop are free by then).
   if constexpr (cm_on) {
-    if (!active) {  // the closed pages
-      closing = vtx::closing_build(cma, cm_pos);
-      n_close = closing.count;
-    }
     vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
                                col);
     if (!active) return;
@@ -269,7 +276,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // per closed page): a wave each, against the fresh centroid
   if constexpr (cm_on) {
     if (n_close > 0 && fix_n > 0) {  // uniform
-      if (!have_mean) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+      if (!have_mean) query_row<LPR, VPL, kQRegs, true>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
       const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
       for (int i = wave; i < fixes; i += kWaves) {
         const int pos = fix_pos[i];
