@@ -61,7 +61,7 @@ HBM_PEAK_GBPS = 8000.0
 # for the probe's copy kernel of known size); the per-launch traffic does not
 # depend on the layer count (34,216 KiB read + 466 KiB written at C2, the
 # launch including the layer's CMean).
-TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_514_368}
+TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_481_568}
 
 
 def _parse():
