@@ -311,6 +311,45 @@ def test_fused_cmean_equals_separate_launches(gpu, name, mode):
 
 
 
+def test_fused_cmean_segment_listing_a_closed_page_many_times(gpu):
+    """A malformed table whose one segment lists the page the launch closes
+    300 times (more than the 256 positions a workgroup re-scores after the
+    loop): the launch completes, every selected id is that page's row, at
+    least 256 copies carry the score against the fresh centroid (the rest the
+    score against the old one), and the centroid is the separate CMean's."""
+    dev = gpu
+    P, D, k, rows = 16, 128, 10, 64
+    c = 37  # the closed page's row (H = 1)
+    n_mid = 300
+    dind = torch.tensor([0, n_mid + 2], dtype=torch.int32, device=dev)
+    sind = torch.tensor([0, k + 2], dtype=torch.int32, device=dev)
+    didx = torch.tensor([5] + [c] * n_mid + [6], dtype=torch.int32, device=dev)
+    sidx = torch.full((k + 2,), -1, dtype=torch.int32, device=dev)
+    loc = torch.tensor([c * P + P - 1], dtype=torch.int64, device=dev)
+    q = W.randn_bf16((1, 2, D), 1, dev)
+    kpool = W.randn_bf16((rows, P, D), 3, dev)
+    y = W.randn_bf16((rows, 1, D), 2, dev, std=0.25)
+    y_ref = y.clone()
+    _hip.page_reduce(kpool, y_ref, loc, 1, P, 1, _hip.REDUCE_MEAN)
+    qm = torch.zeros((1, 1, D), device=dev, dtype=torch.bfloat16)
+    sc = torch.zeros((n_mid + 2, 1, 1), device=dev, dtype=torch.bfloat16)
+    _hip.indexer_fused(q, qm, y, sc, dind, sind, didx, sidx, 1, k, 1, 1, n_mid + 2, mode=_hip.FUSED_SEGMENT,
+                       cmean=(kpool, loc, 1))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    assert (_np(sidx)[1:k + 1] == c).all()
+    def scores_against(cen):
+        out = torch.full_like(sc, -5.0)
+        _hip.indexer_fused(q, None, cen, out, dind, sind, didx, sidx.clone(), 1, k, 1, 1, n_mid + 2,
+                           mode=_hip.FUSED_SEGMENT)
+        torch.cuda.synchronize()
+        return _bits(out)[1:n_mid + 1]
+    fresh, stale = scores_against(y_ref), scores_against(W.randn_bf16((rows, 1, D), 2, dev, std=0.25))
+    got = _bits(sc)[1:n_mid + 1]
+    assert ((got == fresh) | (got == stale)).all()
+    assert (got == fresh).sum() >= 256
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "eos0", "r3", "r9"])
 def test_flow_cmean_carried_into_indexer_launch(gpu, name, monkeypatch):
     """forward_cache's CMean runs inside the next forward_indexer's fused
