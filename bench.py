@@ -193,7 +193,8 @@ class DecodeStep:
                                    ic.sparse_kv_indptr, ic.dense_kv_indices, ic.sparse_kv_indices,
                                    b.batch * b.num_kv_heads, b.topk, b.bos, b.eos,
                                    b.max_pages_per_request, seg_counters=f.output_func.seg_counters,
-                                   mode=fused_layout(), cmean=(k, self.loc, b.num_kv_heads))
+                                   mode=fused_layout(), cmean=(k, self.loc, b.num_kv_heads),
+                                   schedule=ic._fused_schedule)
 
 
 def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: np.ndarray) -> dict:

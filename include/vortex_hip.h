@@ -63,6 +63,14 @@ const char* vtx_version(void);
  * bounds the pages one request can have (ceil(stride / page_size)).
  * Unlike the reference there is no limit on batch_size (reference: 1024 for
  * the indptr scan, 8192 segments for the workload list).
+ *
+ * fused_schedule (optional, NULL for none; no counterpart in the reference):
+ * int32 [fused_schedule_len >= 4 + 4 * batch_size * num_kv_heads], the
+ * workgroup order of vtx_indexer_fused's one-workgroup-per-segment layout:
+ * segments sorted by page count and dealt in snake order over rounds of
+ * schedule_round workgroups (the device's compute-unit count), so that each
+ * compute unit gets a long and a short segment.  Pass it to the indexer
+ * launches of the same step; it changes their speed, never their results.
  */
 int vtx_plan_decode(const int32_t* cached_seq_lens, int32_t batch_size,
                     int32_t* dense_kv_indptr, int32_t* dense_kv_indices,
@@ -77,7 +85,8 @@ int vtx_plan_decode(const int32_t* cached_seq_lens, int32_t batch_size,
                     int32_t num_kv_heads, int32_t topk_val,
                     int32_t page_reserved_bos, int32_t page_reserved_eos,
                     int32_t max_chunk_size, int32_t min_chunk_size,
-                    void* stream);
+                    int32_t* fused_schedule, int64_t fused_schedule_len,
+                    int32_t schedule_round, void* stream);
 
 /*
  * FA3 variant of the decode planner: the block tables, indptrs and workload
@@ -189,6 +198,11 @@ int vtx_topk_select(const uint16_t* score, int64_t score_len,
  * (split when there are fewer than two segments per compute unit and the
  * counters are given), VTX_FUSED_SEGMENT or VTX_FUSED_SPLIT.  Outputs are
  * identical in every mode.
+ *
+ * schedule (optional, NULL for none): the fused_schedule vtx_plan_decode
+ * wrote for this block table.  The segment layout then takes its segments
+ * in that order; each workgroup checks the bounds the schedule holds against
+ * the indptrs, so a schedule from an earlier plan only costs time.
  */
 int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                       const uint16_t* x, uint16_t* x_out, const uint16_t* y,
@@ -199,7 +213,7 @@ int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                       int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                       int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
                       int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
-                      void* stream);
+                      const int32_t* schedule, int64_t schedule_len, void* stream);
 
 /* 1 if vtx_indexer_fused handles this head_dim (64, 128, 256, 512, 576). */
 int vtx_indexer_fused_supported(int32_t head_dim);
@@ -228,7 +242,8 @@ int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_siz
                             int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
                             int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
                             const uint16_t* k_cache, int64_t k_rows, int32_t page_size,
-                            int32_t num_kv_heads, const int64_t* loc, int64_t nnz, void* stream);
+                            int32_t num_kv_heads, const int64_t* loc, int64_t nnz,
+                            const int32_t* schedule, int64_t schedule_len, void* stream);
 
 /*
  * Fused indexer step of the GQA flow: GeMM of the group_size query heads

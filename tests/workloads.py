@@ -205,6 +205,7 @@ def make_contexts(batch: DecodeBatch, device):
     ic.max_num_pages = max(1, batch.dense_capacity())
     ic.max_num_pages_per_request = batch.max_pages_per_request
     ic.topk_val, ic.page_reserved_bos, ic.page_reserved_eos = batch.topk, batch.bos, batch.eos
+    ic._fused_schedule = torch.zeros(4 + 4 * B * H, **i32)
     ic._created = True
     cc = CContext()
     cc.page_size, cc.total_num_pages, cc.head_num, cc.head_dim = P, batch.pool_pages, H, D

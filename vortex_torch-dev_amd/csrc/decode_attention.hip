@@ -69,7 +69,7 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
 
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
-  const int wave = tid / vtx::kWave;
+  const int wave = vtx::uniform(tid / vtx::kWave);
   const int lane = vtx::lane_id();
   const int grp = lane / LPR;
   const int col = lane % LPR;

@@ -34,6 +34,7 @@
 // are the ones gemv.hip uses, so the scores are bit-identical to the GeMV
 // kernel's for the same query.
 #include "vtx_device.h"
+#include "vtx_fused_schedule.h"
 #include "vtx_host.h"
 #include "vtx_cmean.h"
 #include "vtx_page_reduce.h"
@@ -64,6 +65,7 @@ struct FusedArgs {
   int32_t dim;
   int32_t row_cap;   // segments up to this many middle pages are held in LDS
   int32_t segments;  // eff_batch_size; the grid covers all q_rows
+  const int32_t* sched;  // the planner's workgroup schedule (vtx_fused_schedule.h), or null
 };
 
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
@@ -137,20 +139,25 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
   }
 }
 
-// One workgroup per segment: scores into LDS, select in LDS.
+// One workgroup per segment.  When every wave scores at most one pass (the
+// segment has at most waves * kPass middle pages: all of C2), each score
+// stays in the register of the lane that produced it and the selection runs
+// on those registers (vtx::select_regs); longer segments keep their keys in
+// LDS (or re-read their stored scores) and use vtx::select_topk_counted.
 template <int T, int LPR, int VPL, int kCmRegs>
 __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a, vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   constexpr int kPass = vtx::segment_pass<VPL>();
   constexpr int kQRegs = VPL <= 2 ? 2 : 1;  // query rows prefetched
+  // one pass per wave, one position per lane: the register selection
+  constexpr bool kRegSelect = VPL == 1 && (LPR == 8 || LPR == 16) && kPass / kRowsPerLoad == LPR;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
 
-  const int seg = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
-  const int wave = tid / vtx::kWave;
+  const int wave = vtx::uniform(tid / vtx::kWave);
   const int grp = lane / LPR;
   const int col = lane % LPR;
   const int k = a.topk;
@@ -163,11 +170,47 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
 
   // ---- 0. with the in-kernel CMean, loc (issued first, so that waiting for
-  // it waits for nothing else; used once the first row ids are requested)
+  // it waits for nothing else)
   long long cm_pos[kLocRegs];
   if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
 
-  // ---- 1. query rows (issued first: only needed once centroid rows arrive;
+  // ---- 1. this workgroup's segment and its bounds: from the planner's
+  // schedule when its header names this launch (the bounds it holds are a
+  // prediction, checked against the block tables below), else segment
+  // blockIdx.x and the block tables
+  int seg = blockIdx.x;
+  bool predicted = false;
+  int tile_rank = blockIdx.x;  // this workgroup's share of the CMean tiles
+  int32_t pe[3] = {0, 0, 0};   // predicted dense begin, dense end, sparse begin
+  if (a.sched) {               // uniform
+    const int32_t h0 = a.sched[0], h1 = a.sched[1], h2 = a.sched[2];
+    const bool ok = h0 == vtx::kSchedMagic && h1 == a.segments && h2 >= 1;
+    if ((int)blockIdx.x < a.segments) {
+      const int32_t* e = a.sched + 4 + 4 * (long long)blockIdx.x;
+      const int32_t e0 = e[0];
+      pe[0] = e[1];
+      pe[1] = e[2];
+      pe[2] = e[3];
+      if (ok && e0 >= 0 && e0 < a.segments) {
+        seg = e0;
+        predicted = true;
+      }
+    }
+    if (ok) tile_rank = vtx::sched_short_rank32(blockIdx.x, (uint32_t)a.segments, (uint32_t)h2);
+  }
+  const bool is_seg = seg < a.segments;
+  long long start = 0, n = 0, obase = 0;
+  if (predicted) {
+    start = (long long)pe[0] + a.bos;
+    n = (long long)pe[1] - a.eos - start;
+    obase = (long long)pe[2] + a.bos;
+  } else if (is_seg) {
+    start = (long long)a.dindptr[seg] + a.bos;
+    n = (long long)a.dindptr[seg + 1] - a.eos - start;
+    obase = (long long)a.sindptr[seg] + a.bos;
+  }
+
+  // ---- 2. query rows (issued early: only needed once centroid rows arrive;
   // G == 0: the averaged row itself, in qv[0])
   vtx::U4 qv[kQRegs][VPL];
   const bool q_in_regs = a.G <= kQRegs;
@@ -181,94 +224,176 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
         qv[g][v] = g < q_rows_in ? vtx::ld16(qb + (long long)g * D + (v * LPR + col) * 8) : vtx::U4{0u, 0u, 0u, 0u};
   }
 
-  // ---- 2. segment bounds
-  const bool is_seg = seg < a.segments;
-  long long start = 0, n = 0, obase = 0;
-  if (is_seg) {
-    start = (long long)a.dindptr[seg] + a.bos;
-    n = (long long)a.dindptr[seg + 1] - a.eos - start;
-    obase = (long long)a.sindptr[seg] + a.bos;
-  }
-  // pages the in-kernel CMean closes (its loc load overlaps the bounds')
   vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
-  bool active = is_seg && k > 0 && n > k;
-  if (active && (start < 0 || start + n > a.score_len || start + n > a.didx_len || obase < 0 ||
-                 obase + k > a.sidx_len))
-    active = false;
-  const bool cached = active && n <= a.row_cap;
+  auto is_active = [&]() {
+    return is_seg && k > 0 && n > k && start >= 0 && start + n <= a.score_len && start + n <= a.didx_len &&
+           obase >= 0 && obase + k <= a.sidx_len;
+  };
+  bool active = is_active();
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
+  int32_t* sel_pay = reinterpret_cast<int32_t*>(keys + a.row_cap);  // select_regs' payloads
 
-  // ---- 3. query mean (bf16 of the fp32 mean, as torch's mean rounds it);
-  // evaluated after the first row ids are requested so the waits overlap
   float xs[VPL][8];
-  if (!active) {  // uniform over the workgroup
-    if (a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-    if constexpr (!cm_on) return;  // (with the CMean: its tiles first, below)
-  }
-  const int32_t* dseg = a.didx + start;
-  long long share = 0;
-  bool have_mean = false;
-  if constexpr (cm_on) {  // the closed pages (loc arrived with the bounds; loc dies here)
-    closing = vtx::closing_build(cma, cm_pos);
-    n_close = closing.count;
-  }
+  // The pages are split evenly over the waves (one pass each up to
+  // kWaves * kPass pages, so no wave waits on a second round trip while
+  // others idle); row ids come straight from global memory.
+  long long share = 0, p0 = 0;
+  int my_row = -1;  // row ids of the first pass, requested before the CMean tiles
+  auto first_pass = [&]() {
+    share = (n + kWaves - 1) / kWaves;
+    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+    if (share > kPass) share = kPass;
+    p0 = (long long)wave * share;
+    my_row = -1;
+    if (p0 < n) {
+      const int cnt = (int)min(share, n - p0);
+      my_row = lane < cnt ? a.didx[start + p0 + lane] : -1;
+    }
+  };
   if (active) {  // uniform
     vtx::select_init<T>(sel, k, sh);
     if (cm_on && tid == 0) fix_n = 0;
     __syncthreads();  // histogram cleared before any wave counts into it
-
-    if (!q_in_regs) {  // (more than kQRegs rows to average: before the loop)
-      query_row<LPR, VPL, kQRegs>(a, qv, false, qb, seg, store_mean, col, xs);
-      have_mean = true;
-    }
-
-    // ---- 4. scores: the pages are split evenly over the waves (one pass
-    // each up to kWaves * kPass pages, so no wave waits on a second round
-    // trip while others idle); row ids come straight from global memory
-    share = (n + kWaves - 1) / kWaves;
-    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
-    if (share > kPass) share = kPass;
-    for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
-      const int cnt = (int)min(share, n - p0);
-      // one coalesced load of the pass's row ids (lane l holds position l)
-      const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
-      if (!have_mean) {
-        query_row<LPR, VPL, kQRegs, true>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-        have_mean = true;
+    first_pass();
+  }
+  // the segment's bounds from the block tables, in the same round trip
+  int32_t tb[3] = {0, 0, 0};
+  if (predicted) {
+    tb[0] = a.dindptr[seg];
+    tb[1] = a.dindptr[seg + 1];
+    tb[2] = a.sindptr[seg];
+  }
+  // The pages this launch's CMean closes (its tiles are reduced at the end
+  // of the workgroup, see cm_tiles)
+  if constexpr (cm_on) {
+    closing = vtx::closing_build(cma, cm_pos);
+    n_close = closing.count;
+  }
+  // This launch's CMean: wave w of the workgroup of tile rank r reduces tiles
+  // w * grid + r, + waves * grid, ... (one tile per wave 0 for up to `grid`
+  // tiles), after its own segment is done; under a schedule rank 0 is the
+  // workgroup with the shortest segment, so the tiles go to the workgroups
+  // that finish first, while the long segments still stream.  A page whose
+  // centroid it rewrites is scored against the centroid recomputed from its
+  // K tile, so the order against other workgroups' reads does not matter.
+  auto cm_tiles = [&]() {
+    if constexpr (cm_on)
+      vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + tile_rank,
+                                                       kWaves * (int)gridDim.x, grp, col);
+  };
+  if (predicted && (tb[0] != pe[0] || tb[1] != pe[1] || tb[2] != pe[2])) {  // uniform; not for a current schedule
+    const bool was_active = active;
+    start = (long long)tb[0] + a.bos;
+    n = (long long)tb[1] - a.eos - start;
+    obase = (long long)tb[2] + a.bos;
+    active = is_active();
+    if (active) {
+      if (!was_active) {
+        vtx::select_init<T>(sel, k, sh);
+        if (cm_on && tid == 0) fix_n = 0;
+        __syncthreads();
       }
-      int r;
-      const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
-      const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
-      if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
-        // the in-kernel CMean rewrites this page's centroid: scored after the loop
-        const int slot = atomicAdd(&fix_n, 1);
-        if (slot < vtx::kCmLoc) {  // (always, unless the segment lists a page twice)
-          fix_pos[slot] = (int32_t)(p0 + r);
-          r = -1;
-        }
-      }
-      if (r >= 0) {
-        const uint32_t sb = vtx::f32_to_bf16(sc);
-        const uint32_t key = vtx::score_key(sb);
-        a.score[start + p0 + r] = (uint16_t)sb;
-        if (cached) {
-          keys[p0 + r] = (uint16_t)key;
-          rows[p0 + r] = my_rid;
-        }
-        vtx::select_count<T>(key, sh);
-      }
+      first_pass();
     }
   }
-  // This launch's CMean: wave w of workgroup b reduces tiles w * grid + b,
-  // + waves * grid, ... (one tile per wave 0 for up to `grid` tiles), after
-  // its passes (the registers of the scoring loop are free by then).
-  if constexpr (cm_on) {
-    vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x, kWaves * (int)gridDim.x, grp,
-                               col);
-    if (!active) return;
+  if (!active) {
+    if (a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+    cm_tiles();
+    return;
+  }
+  const bool cached = n <= a.row_cap;
+  const int32_t* dseg = a.didx + start;
+
+  bool have_mean = false;
+  if (!q_in_regs) {  // (more than kQRegs rows to average: before the loop)
+    query_row<LPR, VPL, kQRegs>(a, qv, false, qb, seg, store_mean, col, xs);
+    have_mean = true;
+  }
+
+  if constexpr (kRegSelect) {
+    if (n <= (long long)kWaves * kPass) {  // uniform: at most one pass per wave
+      bool have = false, deferred = false;
+      uint32_t key = 0;
+      int rid = -1, r = -1;
+      if (p0 < n) {  // uniform
+        const int cnt = (int)min(share, n - p0);
+        if (!have_mean) {
+          query_row<LPR, VPL, kQRegs, true>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+          have_mean = true;
+        }
+        const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+        rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
+        if (r >= 0) {
+          if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, rid)) {
+            deferred = true;  // this launch's CMean rewrites the page's centroid
+          } else {
+            const uint32_t sb = vtx::f32_to_bf16(sc);
+            key = vtx::score_key(sb);
+            a.score[start + p0 + r] = (uint16_t)sb;
+            vtx::select_count<T>(key, sh);
+            have = true;
+          }
+        }
+      }
+      if constexpr (cm_on) {  // this wave's pages with a rewritten centroid, one at a time
+        uint64_t m = __ballot(deferred);
+        while (m) {  // uniform
+          const int l = __ffsll((long long)m) - 1;
+          m &= m - 1;
+          const int fr = __builtin_amdgcn_readlane(rid, l);
+          const float f = vtx::score_vec<LPR>(vtx::fresh_centroid<LPR>(cma, fr, grp, col), xs);
+          if (lane == l) {
+            const uint32_t sb = vtx::f32_to_bf16(f);
+            key = vtx::score_key(sb);
+            a.score[start + p0 + r] = (uint16_t)sb;
+            vtx::select_count<T>(key, sh);
+            have = true;
+          }
+        }
+      }
+      __syncthreads();  // every key counted
+      vtx::select_regs<T, LPR>(have, key, p0 + r, rid, k, sel, sel_pay, sh,
+                               [&](int rank, int payload) { a.sidx[obase + rank] = payload; });
+      cm_tiles();
+      return;
+    }
+  }
+
+  // ---- 4. scores of longer segments: several passes per wave; keys and row
+  // ids cached in LDS (or the stored scores re-read).  The query mean is
+  // formed first, so the raw query rows are dead inside the loop.
+  if (!have_mean) {
+    query_row<LPR, VPL, kQRegs, true>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+    have_mean = true;
+  }
+  for (bool first = true; p0 < n; p0 += (long long)kWaves * share, first = false) {
+    const int cnt = (int)min(share, n - p0);
+    // one coalesced load of the pass's row ids (lane l holds position l)
+    if (!first) my_row = lane < cnt ? dseg[p0 + lane] : -1;
+    int r;
+    const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+    const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
+    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
+      // the in-kernel CMean rewrites this page's centroid: scored after the loop
+      const int slot = atomicAdd(&fix_n, 1);
+      if (slot < vtx::kCmLoc) {  // (always, unless the segment lists a page twice)
+        fix_pos[slot] = (int32_t)(p0 + r);
+        r = -1;
+      }
+    }
+    if (r >= 0) {
+      const uint32_t sb = vtx::f32_to_bf16(sc);
+      const uint32_t key = vtx::score_key(sb);
+      a.score[start + p0 + r] = (uint16_t)sb;
+      if (cached) {
+        keys[p0 + r] = (uint16_t)key;
+        rows[p0 + r] = my_rid;
+      }
+      vtx::select_count<T>(key, sh);
+    }
   }
   __syncthreads();
 
@@ -276,7 +401,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // per closed page): a wave each, against the fresh centroid
   if constexpr (cm_on) {
     if (n_close > 0 && fix_n > 0) {  // uniform
-      if (!have_mean) query_row<LPR, VPL, kQRegs, true>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
       const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
       for (int i = wave; i < fixes; i += kWaves) {
         const int pos = fix_pos[i];
@@ -305,6 +429,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     vtx::select_topk_counted<T>([&](long long i) { return vtx::score_key(sc[i]); }, n, k, sel, sh);
   }
   vtx::select_emit<T>(sel, k, n, [&](int r, long long pos) { a.sidx[obase + r] = cached ? rows[pos] : dseg[pos]; });
+  cm_tiles();
 }
 
 // Stores / loads performed at device scope (every XCD sees them once the
@@ -339,7 +464,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
 
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
-  const int wave = tid / vtx::kWave;
+  const int wave = vtx::uniform(tid / vtx::kWave);
   const int grp = lane / LPR;
   const int col = lane % LPR;
   const int k = a.topk;
@@ -540,7 +665,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
                int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
                int32_t max_num_pages, int32_t head_dim, int32_t* seg_counters, int64_t seg_counters_len,
-               int32_t mode, const CmeanSpec* cms, void* stream);
+               int32_t mode, const CmeanSpec* cms, const int32_t* schedule, int64_t schedule_len, void* stream);
 
 }  // namespace
 
@@ -553,12 +678,12 @@ extern "C" int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t grou
                                  int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                                  int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
                                  int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
-                                 void* stream) {
+                                 const int32_t* schedule, int64_t schedule_len, void* stream) {
   vtx::clear_error();
   return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
                     sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
                     sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
-                    head_dim, seg_counters, seg_counters_len, mode, nullptr, stream);
+                    head_dim, seg_counters, seg_counters_len, mode, nullptr, schedule, schedule_len, stream);
 }
 
 extern "C" int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
@@ -571,7 +696,7 @@ extern "C" int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_
                                        int32_t head_dim, int32_t* seg_counters, int64_t seg_counters_len,
                                        int32_t mode, const uint16_t* k_cache, int64_t k_rows,
                                        int32_t page_size, int32_t num_kv_heads, const int64_t* loc, int64_t nnz,
-                                       void* stream) {
+                                       const int32_t* schedule, int64_t schedule_len, void* stream) {
   vtx::clear_error();
   if (!k_cache || (nnz > 0 && !loc)) return vtx::fail(VTX_E_INVALID, "indexer_fused_cmean: null K pool or loc");
   if (page_size < 1 || num_kv_heads < 1 || k_rows < 0 || nnz < 0)
@@ -580,7 +705,7 @@ extern "C" int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_
   return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
                     sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
                     sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
-                    head_dim, seg_counters, seg_counters_len, mode, &cm, stream);
+                    head_dim, seg_counters, seg_counters_len, mode, &cm, schedule, schedule_len, stream);
 }
 
 namespace {
@@ -591,7 +716,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
                int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
                int32_t max_num_pages, int32_t head_dim, int32_t* seg_counters, int64_t seg_counters_len,
-               int32_t mode, const CmeanSpec* cms, void* stream) {
+               int32_t mode, const CmeanSpec* cms, const int32_t* schedule, int64_t schedule_len, void* stream) {
   if (eff_batch_size < 0 || group_size < 0 || reserved_bos < 0 || reserved_eos < 0)
     return vtx::fail(VTX_E_INVALID, "indexer_fused: negative size");
   if (!vtx_indexer_fused_supported(head_dim))
@@ -631,6 +756,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   a.eos = reserved_eos;
   a.dim = head_dim;
   a.row_cap = 0;
+  a.sched = nullptr;
 
   if (mode < VTX_FUSED_AUTO || mode > VTX_FUSED_SPLIT)
     return vtx::fail(VTX_E_INVALID, "indexer_fused: unknown mode %d", mode);
@@ -685,12 +811,14 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s);
   }
 
-  const long long room = (kLdsBudget - (long long)a.topk * 8) / 6;
+  // the planner's schedule, when it covers this launch's segments
+  if (schedule && schedule_len >= vtx::sched_len(1, eff_batch_size)) a.sched = schedule;
+  const long long room = (kLdsBudget - (long long)a.topk * 12) / 6;
   long long cap = want < room ? want : room;
   cap &= ~7LL;
   if (cap < 0) cap = 0;
   a.row_cap = (int32_t)cap;
-  const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 6;
+  const size_t lds = (size_t)a.topk * 12 + (size_t)cap * 6;  // + select_regs' payloads
   // With a q_mean output every query row gets a workgroup (rows past the
   // segments only write their mean).
   const long long grid = a.x_out ? q_rows : eff_batch_size;

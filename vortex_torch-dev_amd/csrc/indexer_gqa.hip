@@ -66,7 +66,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
-  const int wave = tid / vtx::kWave;
+  const int wave = vtx::uniform(tid / vtx::kWave);
   const int grp = lane / LPR;
   const int col = lane % LPR;
   const int k = a.topk;

@@ -10,6 +10,7 @@
 // page's first token slot from req_to_token once and writes that page's
 // entry for all H kv heads (consecutive threads -> consecutive addresses).
 #include "vtx_device.h"
+#include "vtx_fused_schedule.h"
 #include "vtx_host.h"
 
 namespace {
@@ -46,6 +47,10 @@ struct PlanArgs {
   int32_t* dcs;
   int32_t* scs;
   int64_t cs_len;
+  // optional: the fused indexer's workgroup schedule (vtx_fused_schedule.h)
+  int32_t* sched;
+  int64_t sched_len;
+  int32_t sched_round;
   int32_t page, heads, topk, bos, eos, chunk;
 };
 
@@ -66,17 +71,19 @@ __device__ __forceinline__ int chunks_of(int n, const PlanArgs& a) {
 }
 
 __global__ __launch_bounds__(kThreads) void plan_decode_kernel(PlanArgs a) {
-  __shared__ long long part[3][kThreads / vtx::kWave];
+  __shared__ long long part[4][kThreads / vtx::kWave];
   const int b = blockIdx.x;
   const int slab = blockIdx.y;
   const int tid = threadIdx.x;
 
+  const bool want_sched = a.sched && a.sched_len >= vtx::sched_len(a.batch, a.heads);
   if (a.batch == 0) {
     if (b == 0 && slab == 0 && tid == 0) {
       a.dense_indptr[0] = 0;
       a.sparse_indptr[0] = 0;
       *a.wnum = 0;
       *a.wchunk = a.chunk;
+      if (want_sched) vtx::sched_write_header(a.sched, 0, a.sched_round);
     }
     return;
   }
@@ -84,35 +91,44 @@ __global__ __launch_bounds__(kThreads) void plan_decode_kernel(PlanArgs a) {
   const int budget = a.topk + a.bos + a.eos;
   const bool head_slab = (slab == 0);
 
-  // Offsets of request b: sums over requests b' < b.
-  long long sd = 0, ss = 0, sc = 0;
-  for (int r = tid; r < b; r += kThreads) {
-    const int n = pages_of(a.seq_lens[r], a.page);
-    sd += n;
-    ss += min(budget, n);
-    if (head_slab) sc += chunks_of(n, a);
+  // Offsets of request b: sums over requests b' < b; with a schedule, also
+  // the request's rank by page count (fewer pages first, ties by index).
+  const int L = a.seq_lens[b];
+  const int n = pages_of(L, a.page);
+  const bool rank_it = head_slab && want_sched;
+  long long sd = 0, ss = 0, sc = 0, rk = 0;
+  const int scan_to = rank_it ? a.batch : b;
+  for (int r = tid; r < scan_to; r += kThreads) {
+    const int nr = pages_of(a.seq_lens[r], a.page);
+    if (r < b) {
+      sd += nr;
+      ss += min(budget, nr);
+      if (head_slab) sc += chunks_of(nr, a);
+    }
+    if (rank_it) rk += (nr < n || (nr == n && r < b)) ? 1 : 0;
   }
   sd = vtx::wave_sum(sd);
   ss = vtx::wave_sum(ss);
   sc = vtx::wave_sum(sc);
+  rk = vtx::wave_sum(rk);
   const int wave = tid / vtx::kWave;
   if (vtx::lane_id() == 0) {
     part[0][wave] = sd;
     part[1][wave] = ss;
     part[2][wave] = sc;
+    part[3][wave] = rk;
   }
   __syncthreads();
-  sd = ss = sc = 0;
+  sd = ss = sc = rk = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / vtx::kWave; ++w) {
     sd += part[0][w];
     ss += part[1][w];
     sc += part[2][w];
+    rk += part[3][w];
   }
 
   const int H = a.heads;
-  const int L = a.seq_lens[b];
-  const int n = pages_of(L, a.page);
   const int sn = min(budget, n);
   const long long dbase = (long long)H * sd;
   const long long sbase = (long long)H * ss;
@@ -147,6 +163,16 @@ __global__ __launch_bounds__(kThreads) void plan_decode_kernel(PlanArgs a) {
         a.wlen[wi] = (k != ck - 1) ? a.chunk : last;
         a.woff[wi] = (int32_t)(dbase + (long long)h * n + (long long)k * a.chunk + a.bos);
       }
+    }
+    if (rank_it) {  // this request's segments in the fused indexer's workgroup order
+      const long long S = (long long)a.batch * H;
+      for (int h = tid; h < H; h += kThreads) {
+        const long long s = (long long)b * H + h;
+        const long long wg = vtx::sched_slot(rk * H + h, S, a.sched_round);
+        vtx::sched_write_entry(a.sched, wg, (int32_t)s, (int32_t)(dbase + (long long)h * n),
+                               (int32_t)(dbase + (long long)(h + 1) * n), (int32_t)(sbase + (long long)h * sn));
+      }
+      if (b == 0 && tid == 0) vtx::sched_write_header(a.sched, (int32_t)S, a.sched_round);
     }
     if (b == a.batch - 1 && tid == 0) {
       const long long s = (long long)a.batch * H;
@@ -197,6 +223,7 @@ int plan_launch(PlanArgs& a, const char* what, const int32_t* cached_seq_lens, i
                 int32_t topk_val, int32_t page_reserved_bos, int32_t page_reserved_eos, int32_t max_chunk_size,
                 void* stream) {
   if (batch_size < 0) return vtx::fail(VTX_E_INVALID, "%s: batch_size < 0", what);
+  if (a.sched && a.sched_round < 1) return vtx::fail(VTX_E_INVALID, "%s: schedule round must be >= 1", what);
   if (page_size < 1 || num_kv_heads < 1 || max_chunk_size < 1)
     return vtx::fail(VTX_E_INVALID,
                      "%s: page_size (%d), num_kv_heads (%d) and max_chunk_size (%d) must be >= 1", what,
@@ -258,10 +285,14 @@ extern "C" int vtx_plan_decode(
     int32_t* winfo_kv_lens, int64_t winfo_capacity, int32_t* winfo_num_workloads,
     int32_t* winfo_chunk_size, int32_t page_size, int32_t num_kv_heads, int32_t topk_val,
     int32_t page_reserved_bos, int32_t page_reserved_eos, int32_t max_chunk_size,
-    int32_t min_chunk_size, void* stream) {
+    int32_t min_chunk_size, int32_t* fused_schedule, int64_t fused_schedule_len, int32_t schedule_round,
+    void* stream) {
   vtx::clear_error();
   (void)min_chunk_size;  // sizes the caller's winfo capacity only
   PlanArgs a{};
+  a.sched = fused_schedule;
+  a.sched_len = fused_schedule ? fused_schedule_len : 0;
+  a.sched_round = schedule_round;
   return plan_launch(a, "plan_decode", cached_seq_lens, batch_size, dense_kv_indptr, dense_kv_indices,
                      dense_kv_indices_len, sparse_kv_indptr, sparse_kv_indices, sparse_kv_indices_len,
                      kv_last_page_len, true, req_to_token, req_to_token_rows, req_to_token_stride, req_indices,

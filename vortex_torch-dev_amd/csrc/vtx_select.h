@@ -31,6 +31,7 @@ template <int T>
 struct SelectShared {
   alignas(16) uint32_t hist[2][256];  // read 16 bytes per lane in sel_find_bin_wave
   uint32_t wave_ties[T / kWave];
+  uint32_t wave_gt[T / kWave];        // select_regs: items above the threshold, per wave
   uint32_t tie_counts[kSelTieTiles * (T / kWave)];  // [tile][wave]
   int count;
 };
@@ -57,8 +58,10 @@ __device__ __forceinline__ long long sel_position(uint64_t c) {
 
 // Run by one full wave (every lane gets the answer): the bin b of `hist`
 // (256 bins, higher = better) holding the kt-th best item, i.e.
-// above(b) < kt <= above(b) + hist[b], and above(b).
-__device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t kt, int* bin, int* above) {
+// above(b) < kt <= above(b) + hist[b], and above(b) (and hist[b] when
+// `count` is given).
+__device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t kt, int* bin, int* above,
+                                                  int* count = nullptr) {
   const int l = lane_id();
   const U4 c = ld16(hist + 4 * l);
   const uint32_t tot = c.x + c.y + c.z + c.w;
@@ -68,24 +71,29 @@ __device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t
   const uint32_t a1 = a2 + c.z;
   const uint32_t a0 = a1 + c.y;
   int b = -1;
-  uint32_t ab = 0;
+  uint32_t ab = 0, cb = 0;
   if (a3 < kt && kt <= a2) {
     b = 4 * l + 3;
     ab = a3;
+    cb = c.w;
   } else if (a2 < kt && kt <= a1) {
     b = 4 * l + 2;
     ab = a2;
+    cb = c.z;
   } else if (a1 < kt && kt <= a0) {
     b = 4 * l + 1;
     ab = a1;
+    cb = c.y;
   } else if (a0 < kt && kt <= a0 + c.x) {
     b = 4 * l;
     ab = a0;
+    cb = c.x;
   }
   const uint64_t m = __ballot(b >= 0);
   const int src = m ? (int)__builtin_ctzll(m) : 0;
   *bin = m ? (int)lane_value((uint32_t)b, src) : 0;
   *above = m ? (int)lane_value(ab, src) : 0;
+  if (count) *count = m ? (int)lane_value(cb, src) : 0;
 }
 
 // Clears the histograms, the winner count and the winner slots (no barrier).
@@ -250,6 +258,105 @@ __device__ __forceinline__ int rank_of(uint64_t c, const uint64_t* sel, int k) {
   }
   for (; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
   return r;
+}
+
+// Output rank of winner `c` among the k winners in sel, reading two
+// composites per 16-byte broadcast read (sel 16-byte aligned).
+__device__ __forceinline__ int rank_of_pairs(uint64_t c, const uint64_t* sel, int k) {
+  int r = 0;
+  int m = 0;
+  for (; m + 16 <= k; m += 16) {
+    U4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = ld16(sel + m + 2 * u);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      r += (((uint64_t)v[u].y << 32 | v[u].x) > c) ? 1 : 0;
+      r += (((uint64_t)v[u].w << 32 | v[u].z) > c) ? 1 : 0;
+    }
+  }
+  for (; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
+  return r;
+}
+
+// Position rank inside a wave of the scoring layout in which lane
+// l = grp * LPR + col holds pass position col * (64 / LPR) + grp: the number
+// of lanes in `m` whose position is below this lane's.
+template <int LPR>
+__device__ __forceinline__ int pass_rank_below(uint64_t m) {
+  constexpr int kGroups = kWave / LPR;
+  constexpr uint64_t kRep = LPR == 16 ? 0x0001000100010001ull : (LPR == 8 ? 0x0101010101010101ull : 0ull);
+  static_assert(kRep != 0, "pass_rank_below: LPR 8 or 16");
+  static_assert(kGroups * LPR == kWave, "lane layout");
+  const int l = lane_id();
+  const int grp = l / LPR, col = l % LPR;
+  const uint64_t lower_col = ((1ull << col) - 1ull) * kRep;                       // col' < col
+  const uint64_t same_col = ((1ull << col) * kRep) & ((1ull << (grp * LPR)) - 1ull);  // col' == col, grp' < grp
+  return __popcll(m & lower_col) + __popcll(m & same_col);
+}
+
+// Selection of the k best items (largest key first, ties to the lower
+// position) when every item is held in registers by one thread: `have`,
+// its 16-bit order key, its position and a payload.  The items of wave w
+// have lower positions than those of wave w + 1, and inside a wave they
+// follow the scoring layout of pass_rank_below<LPR>.  hist[0] must hold the
+// high-byte counts of every item and hist[1] zeros, visible after a barrier.
+//
+//   1. the threshold key thr from the two 8-bit histogram passes (the same
+//      passes as select_topk_counted);
+//   2. per-wave counts of the items above thr and equal to thr (one LDS
+//      exchange) give each item above thr a winner slot and each tie its
+//      rank in position order; the first `take` ties win;
+//   3. each winner's output rank is the number of winners with a larger
+//      composite (key << 32 | ~position).
+// emit(rank, payload) is called once per winner.  sel holds k composites,
+// sel_pay k payloads (LDS, 16-byte aligned).  Requires 0 < k < n; every
+// thread of the workgroup calls it (it contains barriers).
+template <int T, int LPR, typename Emit>
+__device__ __forceinline__ void select_regs(bool have, uint32_t key, long long pos, int payload, int k,
+                                            uint64_t* sel, int32_t* sel_pay, SelectShared<T>& sh, Emit emit) {
+  constexpr int kWaves = T / kWave;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  int hi = 0, above_hi = 0;
+  sel_find_bin_wave(sh.hist[0], (uint32_t)k, &hi, &above_hi);
+  if (have && (key >> 8) == (uint32_t)hi) atomicAdd(&sh.hist[1][key & 255u], 1u);
+  __syncthreads();
+  int lo = 0, above_lo = 0;
+  sel_find_bin_wave(sh.hist[1], (uint32_t)(k - above_hi), &lo, &above_lo);
+  const uint32_t thr = ((uint32_t)hi << 8) | (uint32_t)lo;
+  const int above = above_hi + above_lo;  // items with a key above thr
+  const int take = k - above;             // >= 1 of the items equal to thr win
+  const bool gt = have && key > thr;
+  const bool tie = have && key == thr;
+  const uint64_t mg = __ballot(gt);
+  const uint64_t mt = __ballot(tie);
+  if (lane == 0) {
+    sh.wave_gt[wave] = (uint32_t)__popcll(mg);
+    sh.wave_ties[wave] = (uint32_t)__popcll(mt);
+  }
+  __syncthreads();
+  int gt_before = 0, tie_before = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) {
+      gt_before += (int)sh.wave_gt[w];
+      tie_before += (int)sh.wave_ties[w];
+    }
+  }
+  const int tie_rank = tie_before + pass_rank_below<LPR>(mt);
+  const bool win = gt || (tie && tie_rank < take);
+  const int slot = gt ? gt_before + lanes_below(mg) : above + tie_rank;
+  if (win) {
+    sel[slot] = sel_composite(key, pos);
+    sel_pay[slot] = payload;
+  }
+  __syncthreads();
+  for (int j = tid; j < k; j += T) {
+    const uint64_t c = sel[j];
+    emit(rank_of_pairs(c, sel, k), sel_pay[j]);
+  }
 }
 
 // Calls emit(rank, position) for every winner (rank 0 = best).

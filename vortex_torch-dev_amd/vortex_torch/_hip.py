@@ -31,7 +31,7 @@ _SIGNATURES = {
     "vtx_version": ([], ctypes.c_char_p),
     "vtx_plan_decode": (
         [_vp, _i32, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp,
-         _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+         _i64, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
         ctypes.c_int,
     ),
     "vtx_plan_decode_fa3": (
@@ -57,13 +57,13 @@ _SIGNATURES = {
     ),
     "vtx_indexer_fused": (
         [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _vp],
         ctypes.c_int,
     ),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
     "vtx_indexer_fused_cmean": (
         [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i64, _vp],
         ctypes.c_int,
     ),
     "vtx_indexer_gqa_fused": (
@@ -225,6 +225,17 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+_cu_counts: dict = {}
+
+
+def device_cu_count(dev: torch.device) -> int:
+    """Compute units of `dev` (cached)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _cu_counts:
+        _cu_counts[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _cu_counts[idx]
+
+
 class _on_device:
     """Makes `dev` current for the duration of a launch (no-op if it already is)."""
 
@@ -271,13 +282,19 @@ def plan_decode(
     page_reserved_eos: int,
     max_chunk_size: int,
     min_chunk_size: int,
+    fused_schedule=None,
+    schedule_round: int = 0,
 ) -> None:
+    """Decode planner (vtx_plan_decode).  fused_schedule (optional int32
+    buffer of at least 4 + 4 * B * H entries): also write the fused indexer's
+    workgroup order for this block table, dealt in rounds of schedule_round
+    workgroups (the device's compute-unit count; 0 = this device's)."""
     lib = load_library()
     i32 = torch.int32
     dev = _require_gpu(cached_seq_lens, dense_kv_indptr, dense_kv_indices, sparse_kv_indptr,
                        sparse_kv_indices, kv_last_page_len, req_to_token, req_indices,
                        winfo_q_indices, winfo_kv_offsets, winfo_kv_lens, winfo_num_workloads,
-                       winfo_chunk_size)
+                       winfo_chunk_size, *([fused_schedule] if fused_schedule is not None else []))
     for t, n in ((cached_seq_lens, "cached_seq_lens"), (dense_kv_indptr, "dense_kv_indptr"),
                  (dense_kv_indices, "dense_kv_indices"), (sparse_kv_indptr, "sparse_kv_indptr"),
                  (sparse_kv_indices, "sparse_kv_indices"), (kv_last_page_len, "kv_last_page_len"),
@@ -299,6 +316,12 @@ def plan_decode(
     if winfo_num_workloads.numel() < 1 or winfo_chunk_size.numel() < 1:
         raise RuntimeError("vortex_torch: winfo_num_workloads / winfo_chunk_size need 1 entry")
     wcap = min(winfo_q_indices.numel(), winfo_kv_offsets.numel(), winfo_kv_lens.numel())
+    sched_ptr, sched_len, sched_round = None, 0, 0
+    if fused_schedule is not None:
+        _req(fused_schedule, i32, "fused_schedule")
+        if fused_schedule.numel() >= 4 + 4 * B * H:  # (too small: no schedule)
+            sched_ptr, sched_len = fused_schedule.data_ptr(), fused_schedule.numel()
+            sched_round = int(schedule_round) if schedule_round else device_cu_count(dev)
     with _on_device(dev):
         rc = lib.vtx_plan_decode(
             cached_seq_lens.data_ptr(), B,
@@ -310,7 +333,7 @@ def plan_decode(
             winfo_q_indices.data_ptr(), winfo_kv_offsets.data_ptr(), winfo_kv_lens.data_ptr(), wcap,
             winfo_num_workloads.data_ptr(), winfo_chunk_size.data_ptr(),
             int(page_size), H, int(topk_val), int(page_reserved_bos), int(page_reserved_eos),
-            int(max_chunk_size), int(min_chunk_size), _stream(dev))
+            int(max_chunk_size), int(min_chunk_size), sched_ptr, sched_len, sched_round, _stream(dev))
     _check(rc, "plan_decode")
 
 
@@ -538,6 +561,7 @@ def indexer_fused(
     seg_counters=None,
     mode: int = FUSED_AUTO,
     cmean=None,
+    schedule=None,
 ) -> None:
     """q-mean + GeMV + topK of one layer in one launch.
 
@@ -550,10 +574,14 @@ def indexer_fused(
     FUSED_SEGMENT or FUSED_SPLIT.  cmean: (k_cache [rows, P, D] bf16, loc
     int64, num_kv_heads) — the layer's page-finish mean into y, run first in
     the same launch (``vtx_indexer_fused_cmean``), with the results of a
-    separate ``page_reduce`` launch before this one.
+    separate ``page_reduce`` launch before this one.  schedule: the
+    fused_schedule plan_decode wrote for this block table (the workgroup
+    order of the one-workgroup-per-segment layout; speed only).
     """
     lib = load_library()
     tensors = [q, y, score, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
+    if schedule is not None:
+        tensors.append(schedule)
     if cmean is not None:
         tensors += [cmean[0], cmean[1]]
     if x_out is not None:
@@ -594,6 +622,9 @@ def indexer_fused(
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), D,
             seg_counters.data_ptr() if seg_counters is not None else None,
             seg_counters.numel() if seg_counters is not None else 0, int(mode))
+    if schedule is not None:
+        _req(schedule, torch.int32, "schedule")
+    sched = (schedule.data_ptr() if schedule is not None else None, schedule.numel() if schedule is not None else 0)
     if cmean is not None:
         k, loc, heads = cmean
         _req(k, torch.bfloat16, "k_cache")
@@ -603,11 +634,11 @@ def indexer_fused(
                                f"do not match head_dim {D}")
         with _on_device(dev):
             rc = lib.vtx_indexer_fused_cmean(*args, k.data_ptr(), int(k.shape[0]), int(k.shape[1]), int(heads),
-                                             loc.data_ptr(), loc.numel(), _stream(dev))
+                                             loc.data_ptr(), loc.numel(), *sched, _stream(dev))
         _check(rc, "indexer_fused_cmean")
         return
     with _on_device(dev):
-        rc = lib.vtx_indexer_fused(*args, _stream(dev))
+        rc = lib.vtx_indexer_fused(*args, *sched, _stream(dev))
     _check(rc, "indexer_fused")
 
 

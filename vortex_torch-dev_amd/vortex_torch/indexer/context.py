@@ -42,7 +42,9 @@ def _compute_units() -> int:
 class Context(ContextBase):
     """Mutable single-instance context, populated by :meth:`create`."""
 
-    __slots__ = ContextBase.__slots__ + _FIELDS + ("_aux_total_bytes", "_aux_total_flops")
+    # _fused_schedule: int32 buffer the decode planner fills with the fused
+    # indexer's workgroup order (speed only; not a reference field)
+    __slots__ = ContextBase.__slots__ + _FIELDS + ("_aux_total_bytes", "_aux_total_flops", "_fused_schedule")
 
     def __init__(self) -> None:
         for n in self.__slots__:
@@ -53,6 +55,7 @@ class Context(ContextBase):
         self.batch_size = 0
         self._aux_total_bytes = 0
         self._aux_total_flops = 0
+        self._fused_schedule = None
 
     def set_batch_size(self, n: int) -> None:
         self.batch_size = n
@@ -108,6 +111,7 @@ class Context(ContextBase):
         self.winfo_kv_lens = torch.zeros((n,), dtype=torch.int32, device=device)
         self.winfo_num_workloads = torch.zeros((1,), dtype=torch.int32, device=device)
         self.winfo_chunk_size = torch.zeros((1,), dtype=torch.int32, device=device)
+        self._fused_schedule = torch.zeros((4 + 4 * max_bs * self.num_kv_heads,), dtype=torch.int32, device=device)
 
         self._created = True
         return self

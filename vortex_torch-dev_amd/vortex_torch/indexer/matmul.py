@@ -67,12 +67,19 @@ class PendingGemv(_deferred.Pending):
             ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
             ctx.page_reserved_eos, ctx.max_num_pages_per_request, seg_counters=seg_counters,
             mode=_deferred.fused_layout(),
-            cmean=None if cm is None else (cm.x, cm.loc, cm.ctx.head_num))
+            cmean=None if cm is None else (cm.x, cm.loc, cm.ctx.head_num),
+            schedule=_schedule_of(ctx))
         if cm is not None:
             cm.done = True
         if mean is not None:
             mean.done = True
         self.done = True
+
+
+def _schedule_of(ctx: Context) -> Optional[torch.Tensor]:
+    """The fused-indexer schedule plan_decode wrote into the context, if any."""
+    s = getattr(ctx, "_fused_schedule", None)
+    return s if isinstance(s, torch.Tensor) and s.is_cuda else None
 
 
 def _fusable(x: torch.Tensor, y: torch.Tensor, ctx: Context) -> bool:

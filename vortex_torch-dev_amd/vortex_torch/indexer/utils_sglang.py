@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from .. import _C
+from .. import _C, _hip
 from .context import Context
 
 
@@ -22,7 +22,12 @@ def plan_decode(
     req_indices: torch.Tensor,
     ctx: Context,
 ) -> None:
-    _C.sglang_plan_decode(
+    """Reference: vortex_torch/indexer/utils_sglang.py:15-44.  The same
+    launch also writes the context's fused-indexer schedule (the workgroup
+    order that pairs long with short segments on each compute unit), which the
+    fused indexer launches of this step read."""
+    sched = getattr(ctx, "_fused_schedule", None)
+    _hip.plan_decode(
         cached_seq_lens,
         ctx.dense_kv_indptr,
         ctx.dense_kv_indices,
@@ -43,6 +48,7 @@ def plan_decode(
         ctx.page_reserved_eos,
         ctx.max_chunk_size,
         ctx.min_chunk_size,
+        fused_schedule=sched if isinstance(sched, torch.Tensor) else None,
     )
     ctx.set_batch_size(cached_seq_lens.shape[0])
 
