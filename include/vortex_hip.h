@@ -40,6 +40,16 @@ const char* vtx_last_error(void);
 const char* vtx_version(void);
 
 /*
+ * *id = 0 if `stream` is not being captured into a graph, otherwise a value
+ * that identifies the capture in progress (the same for every stream taking
+ * part in it, different for every capture).  Host-side query, no launch.
+ * No counterpart in the reference: the Python layer uses it to keep work it
+ * records for a later launch (the page-finish mean a flow's forward_cache
+ * leaves for the next forward_indexer) inside the capture it was recorded in.
+ */
+int vtx_stream_capture_id(void* stream, unsigned long long* id);
+
+/*
  * Decode planner: builds the per-step dense/sparse block tables and the GeMV
  * workload list for all sparse layers.
  *

@@ -248,3 +248,46 @@ def test_carry_off(carry_launches, monkeypatch):
     assert carry_launches == ["page_reduce"]
     layer.indexer_step()
     assert carry_launches == ["page_reduce", "indexer_fused"]
+
+
+# ------------------------------------------------------------ graph capture
+def test_capture_boundaries_launch_the_carry(carry_launches):
+    """torch.cuda.CUDAGraph.capture_begin / capture_end launch a carried mean
+    before torch's own method runs (here it then fails on a non-graph)."""
+    layer = _Layer()
+    layer.cache_step()
+    assert carry_launches == []
+    with pytest.raises(TypeError):
+        torch.cuda.CUDAGraph.capture_end(object())
+    assert carry_launches == ["page_reduce"]
+    layer.cache_step()
+    with pytest.raises(TypeError):
+        torch.cuda.CUDAGraph.capture_begin(object())
+    assert carry_launches == ["page_reduce", "page_reduce"]
+    assert _deferred.current_carry() is None
+
+
+def test_carry_across_a_capture_boundary_is_an_error(carry_launches, monkeypatch):
+    state = {"id": 0}
+    monkeypatch.setattr(_deferred, "_capture_of", lambda stream: state["id"])
+    layer = _Layer()
+    state["id"] = 5  # recorded during capture 5 ...
+    layer.cache_step()
+    state["id"] = 0  # ... which ended without launching it
+    with pytest.raises(RuntimeError, match="recorded during a graph capture and would now be launched outside"):
+        layer.indexer_step()
+    layer.cache_step()  # recorded outside any capture ...
+    state["id"] = 9  # ... found inside one
+    with pytest.raises(RuntimeError, match="recorded outside any graph capture and would now be launched during"):
+        layer.indexer_step()
+    state["id"] = 3
+    layer.cache_step()
+    state["id"] = 4  # another capture
+    with pytest.raises(RuntimeError, match="in another capture"):
+        _deferred.flush_carry()
+    assert "page_reduce" not in carry_launches  # never launched where it does not belong
+    state["id"] = 6
+    layer.cache_step()
+    carry_launches.clear()
+    layer.indexer_step()  # same capture: consumed
+    assert carry_launches == ["indexer_fused+cmean"]

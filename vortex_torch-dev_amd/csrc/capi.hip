@@ -52,3 +52,15 @@ int device_cu_count() {
 extern "C" const char* vtx_last_error(void) { return vtx::g_last_error.c_str(); }
 
 extern "C" const char* vtx_version(void) { return "vortex-mi355x 0.1.0 (gfx950)"; }
+
+extern "C" int vtx_stream_capture_id(void* stream, unsigned long long* id) {
+  vtx::clear_error();
+  if (!id) return vtx::fail(VTX_E_INVALID, "vtx_stream_capture_id: id is null");
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  hipError_t e = hipStreamGetCaptureInfo((hipStream_t)stream, &status, &cid);
+  if (e != hipSuccess)
+    return vtx::fail(VTX_E_DEVICE, "vtx_stream_capture_id: %s", hipGetErrorString(e));
+  *id = status == hipStreamCaptureStatusActive ? cid + 1 : 0;
+  return VTX_OK;
+}

@@ -169,6 +169,17 @@ def current_scope() -> Optional[Scope]:
 # provided the centroid pool and the K pool are only touched through this
 # package or through torch on their vTensors between the two calls — as in
 # a decode layer, where forward_indexer follows forward_cache.
+#
+# Graph capture.  A carry belongs to the capture it was recorded in (or to
+# none): it is launched into that capture or, recorded outside any, before a
+# capture starts.  torch.cuda.CUDAGraph.capture_begin and capture_end (which
+# torch.cuda.graph and make_graphed_callables call) launch the carry first, so
+# a capture never ends with a carried mean outside the graph, whatever the
+# order of the flow's calls within it (forward_indexer may precede
+# forward_cache: the last layer's carry then lands at the end of the graph).
+# A carry found on a stream whose capture state has changed by other means
+# (a capture begun or ended outside these two methods) is an error, raised
+# instead of launching the mean outside the work it belongs to.
 
 
 def _carry_enabled() -> bool:
@@ -183,13 +194,35 @@ def _stream_of(dev: torch.device):
     return torch.cuda.current_stream(dev) if dev.type == "cuda" else None
 
 
+def _capture_of(stream) -> int:
+    """Id of the graph capture `stream` takes part in (0: none)."""
+    if stream is None:
+        return 0
+    from . import _hip
+
+    return _hip.stream_capture_id(stream)
+
+
+def _check_capture(carry) -> None:
+    pending, stream, cap = carry
+    now = _capture_of(stream)
+    if now != cap:
+        where = {True: "during a graph capture", False: "outside any graph capture"}
+        raise RuntimeError(
+            "vortex_torch: a page-finish mean that forward_cache left for the next forward_indexer was "
+            f"recorded {where[cap != 0]} and would now be launched "
+            f"{'in another capture' if cap and now else where[now != 0]}; begin and end captures with "
+            "torch.cuda.graph / torch.cuda.CUDAGraph (which launch it first), or set VORTEX_FUSE_CMEAN=0")
+
+
 def flush_carry() -> None:
     """Launches the carried page-finish mean, if any, on its own stream."""
     c = current_carry()
     if c is None:
         return
     _tls.carry = None
-    pending, stream = c
+    _check_capture(c)
+    pending, stream, _ = c
     with (torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()):
         pending.flush()
 
@@ -226,8 +259,8 @@ def _take_if(ok) -> Optional[Pending]:
     c = current_carry()
     if c is None:
         return None
-    pending, stream = c
-    if not ok(pending) or _stream_of(pending.x.device) != stream:
+    pending, stream, cap = c
+    if not ok(pending) or _stream_of(pending.x.device) != stream or _capture_of(stream) != cap:
         flush_carry()
         return None
     _tls.carry = None
@@ -278,7 +311,8 @@ def scope(active: bool, kind: str = "indexer"):
             if (kind == "cache" and _carry_enabled() and len(sc.pending) == 1
                     and getattr(sc.pending[0], "carryable", lambda: False)()):
                 p = sc.pending.pop()
-                _tls.carry = (p, _stream_of(p.x.device))
+                st = _stream_of(p.x.device)
+                _tls.carry = (p, st, _capture_of(st))
             sc.flush()
             if kind == "indexer":
                 flush_carry()
@@ -414,4 +448,29 @@ def _install_launch_hook() -> None:
     _hip.set_pre_launch_hook(flush_carry)
 
 
+def _install_capture_hooks() -> None:
+    """Makes torch.cuda.CUDAGraph.capture_begin / capture_end launch the carry
+    first (see "Graph capture" above)."""
+    import functools
+
+    graph = getattr(torch.cuda, "CUDAGraph", None)
+    if graph is None or getattr(graph, "_vortex_carry_hooks", False):
+        return
+    begin, end = graph.capture_begin, graph.capture_end
+
+    @functools.wraps(begin)
+    def capture_begin(self, *args, **kwargs):
+        flush_carry()
+        return begin(self, *args, **kwargs)
+
+    @functools.wraps(end)
+    def capture_end(self, *args, **kwargs):
+        flush_carry()
+        return end(self, *args, **kwargs)
+
+    graph.capture_begin, graph.capture_end = capture_begin, capture_end
+    graph._vortex_carry_hooks = True
+
+
 _install_launch_hook()
+_install_capture_hooks()

@@ -116,6 +116,7 @@ _SIGNATURES = {
     ),
     "vtx_paged_decode_attention_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_bf16_rounding_check": ([_vp, _vp], ctypes.c_int),
+    "vtx_stream_capture_id": ([_vp, ctypes.POINTER(ctypes.c_ulonglong)], ctypes.c_int),
     "vtx_segment_scan": (
         [_i32, ctypes.c_float, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
@@ -223,6 +224,15 @@ def _req(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
 
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
+
+
+def stream_capture_id(stream) -> int:
+    """0 if the torch stream `stream` is not being captured into a graph, else
+    an id of the capture in progress (host-side query, no launch)."""
+    lib = load_library()
+    out = ctypes.c_ulonglong(0)
+    _check(lib.vtx_stream_capture_id(stream.cuda_stream, ctypes.byref(out)), "stream_capture_id")
+    return int(out.value)
 
 
 _cu_counts: dict = {}
