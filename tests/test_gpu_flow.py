@@ -311,43 +311,62 @@ def test_fused_cmean_equals_separate_launches(gpu, name, mode):
 
 
 
-def test_fused_cmean_segment_listing_a_closed_page_many_times(gpu):
+@pytest.mark.parametrize("kernel", ["mean", "gqa", "quest"])
+def test_fused_cmean_segment_listing_a_closed_page_many_times(gpu, kernel):
     """A malformed table whose one segment lists the page the launch closes
-    300 times (more than the 256 positions a workgroup re-scores after the
-    loop): the launch completes, every selected id is that page's row, at
-    least 256 copies carry the score against the fresh centroid (the rest the
-    score against the old one), and the centroid is the separate CMean's."""
+    300 times: the launch with the in-kernel page-finish reduction writes
+    exactly what the separate reduction followed by the same kernel writes —
+    every copy scored against the fresh centroid (or envelopes), none against
+    a row being rewritten — for the q-mean, GQA and Quest kernels."""
     dev = gpu
     P, D, k, rows = 16, 128, 10, 64
+    G = 2 if kernel == "mean" else 4
     c = 37  # the closed page's row (H = 1)
     n_mid = 300
     dind = torch.tensor([0, n_mid + 2], dtype=torch.int32, device=dev)
     sind = torch.tensor([0, k + 2], dtype=torch.int32, device=dev)
     didx = torch.tensor([5] + [c] * n_mid + [6], dtype=torch.int32, device=dev)
-    sidx = torch.full((k + 2,), -1, dtype=torch.int32, device=dev)
     loc = torch.tensor([c * P + P - 1], dtype=torch.int64, device=dev)
-    q = W.randn_bf16((1, 2, D), 1, dev)
+    q = W.randn_bf16((1, G, D), 1, dev)
     kpool = W.randn_bf16((rows, P, D), 3, dev)
-    y = W.randn_bf16((rows, 1, D), 2, dev, std=0.25)
-    y_ref = y.clone()
-    _hip.page_reduce(kpool, y_ref, loc, 1, P, 1, _hip.REDUCE_MEAN)
-    qm = torch.zeros((1, 1, D), device=dev, dtype=torch.bfloat16)
-    sc = torch.zeros((n_mid + 2, 1, 1), device=dev, dtype=torch.bfloat16)
-    _hip.indexer_fused(q, qm, y, sc, dind, sind, didx, sidx, 1, k, 1, 1, n_mid + 2, mode=_hip.FUSED_SEGMENT,
-                       cmean=(kpool, loc, 1))
-    torch.cuda.synchronize()
-    assert torch.equal(y, y_ref)
-    assert (_np(sidx)[1:k + 1] == c).all()
-    def scores_against(cen):
-        out = torch.full_like(sc, -5.0)
-        _hip.indexer_fused(q, None, cen, out, dind, sind, didx, sidx.clone(), 1, k, 1, 1, n_mid + 2,
-                           mode=_hip.FUSED_SEGMENT)
+    pools0 = [W.randn_bf16((rows, 1, D), 2 + i, dev, std=0.25) for i in range(2 if kernel == "quest" else 1)]
+    table = (dind, sind, didx)
+
+    def run(in_launch):
+        pools = [t.clone() for t in pools0]
+        sidx = torch.full((k + 2,), -1, dtype=torch.int32, device=dev)
+        if kernel == "mean":
+            outs = [torch.zeros((1, 1, D), device=dev, dtype=torch.bfloat16),
+                    torch.full((n_mid + 2, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)]
+            if not in_launch:
+                _hip.page_reduce(kpool, pools[0], loc, 1, P, 1, _hip.REDUCE_MEAN)
+            _hip.indexer_fused(q, outs[0], pools[0], outs[1], *table[:2], didx, sidx, 1, k, 1, 1, n_mid + 2,
+                               mode=_hip.FUSED_SEGMENT, cmean=(kpool, loc, 1) if in_launch else None)
+        elif kernel == "gqa":
+            outs = [torch.full((n_mid + 2, 1, G), -5.0, device=dev, dtype=torch.bfloat16),
+                    torch.full((n_mid + 2, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)]
+            if not in_launch:
+                _hip.page_reduce(kpool, pools[0], loc, 1, P, 1, _hip.REDUCE_MEAN)
+            _hip.indexer_gqa_fused(q, pools[0], outs[0], outs[1], *table[:2], didx, sidx, 1, k, 1, 1, n_mid + 2,
+                                   softmax_scale=0.09, cmean=(kpool, loc, 1) if in_launch else None)
+        else:
+            outs = [torch.full((n_mid + 2, G, 1), -5.0, device=dev, dtype=torch.bfloat16),
+                    torch.full((n_mid + 2, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)]
+            if not in_launch:
+                _hip.page_reduce_multi(kpool, pools, [_hip.REDUCE_MAX, _hip.REDUCE_MIN], loc, 1, P, 1)
+            _hip.indexer_quest_fused(q, pools[0], pools[1], outs[0], outs[1], *table[:2], didx, sidx, 1, k, 1, 1,
+                                     n_mid + 2, envelope=(kpool, loc, 1) if in_launch else None)
         torch.cuda.synchronize()
-        return _bits(out)[1:n_mid + 1]
-    fresh, stale = scores_against(y_ref), scores_against(W.randn_bf16((rows, 1, D), 2, dev, std=0.25))
-    got = _bits(sc)[1:n_mid + 1]
-    assert ((got == fresh) | (got == stale)).all()
-    assert (got == fresh).sum() >= 256
+        return [_bits(t) for t in pools + outs] + [_np(sidx)]
+
+    sep, fused = run(False), run(True)
+    assert (sep[0] != _bits(pools0[0])).any(), "the reduction changed nothing"
+    for a, b in zip(sep, fused):
+        np.testing.assert_array_equal(a, b)
+    assert (fused[-1][1:k + 1] == c).all()
+    # every copy of the page carries one score, the fresh one
+    score = (fused[-2] if kernel == "mean" else fused[-3]).reshape(n_mid + 2, -1)[1:n_mid + 1]
+    assert (score == score[0]).all()
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "eos0", "r3", "r9"])

@@ -163,8 +163,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int k = a.topk;
   const int D = a.dim;
   const bool store_mean = wave == 0 && grp == 0;
-  __shared__ int32_t fix_pos[vtx::kCmLoc];  // middle positions scored in step 4b
-  __shared__ int fix_n;
   // kCmRegs > 0: this launch runs the layer's CMean over up to 64 * kCmRegs loc entries
   constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
@@ -255,7 +253,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   };
   if (active) {  // uniform
     vtx::select_init<T>(sel, k, sh);
-    if (cm_on && tid == 0) fix_n = 0;
     __syncthreads();  // histogram cleared before any wave counts into it
     first_pass();
   }
@@ -293,7 +290,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     if (active) {
       if (!was_active) {
         vtx::select_init<T>(sel, k, sh);
-        if (cm_on && tid == 0) fix_n = 0;
         __syncthreads();
       }
       first_pass();
@@ -374,14 +370,20 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     // one coalesced load of the pass's row ids (lane l holds position l)
     if (!first) my_row = lane < cnt ? dseg[p0 + lane] : -1;
     int r;
-    const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+    float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);  // row id of this lane's page
-    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
-      // the in-kernel CMean rewrites this page's centroid: scored after the loop
-      const int slot = atomicAdd(&fix_n, 1);
-      if (slot < vtx::kCmLoc) {  // (always, unless the segment lists a page twice)
-        fix_pos[slot] = (int32_t)(p0 + r);
-        r = -1;
+    if constexpr (cm_on) {
+      if (n_close > 0) {  // uniform
+        // pages whose centroid this launch's CMean rewrites: scored against
+        // the centroid recomputed from the K tile, one at a time per wave
+        uint64_t m = __ballot(vtx::closes_here(cma, closing, r, my_rid));
+        while (m) {  // uniform
+          const int l = __ffsll((long long)m) - 1;
+          m &= m - 1;
+          const int fr = __builtin_amdgcn_readlane(my_rid, l);
+          const float f = vtx::score_vec<LPR>(vtx::fresh_centroid<LPR>(cma, fr, grp, col), xs);
+          if (lane == l) sc = f;
+        }
       }
     }
     if (r >= 0) {
@@ -396,30 +398,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     }
   }
   __syncthreads();
-
-  // ---- 4b. pages whose centroid this launch's CMean rewrites (at most one
-  // per closed page): a wave each, against the fresh centroid
-  if constexpr (cm_on) {
-    if (n_close > 0 && fix_n > 0) {  // uniform
-      const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
-      for (int i = wave; i < fixes; i += kWaves) {
-        const int pos = fix_pos[i];
-        const int rid = dseg[pos];
-        const float f = vtx::score_vec<LPR>(vtx::fresh_centroid<LPR>(cma, rid, grp, col), xs);
-        if (lane == 0) {
-          const uint32_t sb = vtx::f32_to_bf16(f);
-          const uint32_t key = vtx::score_key(sb);
-          a.score[start + pos] = (uint16_t)sb;
-          if (cached) {
-            keys[pos] = (uint16_t)key;
-            rows[pos] = rid;
-          }
-          vtx::select_count<T>(key, sh);
-        }
-      }
-      __syncthreads();
-    }
-  }
 
   // ---- 5. top-k of the segment
   if (cached) {

@@ -60,8 +60,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
 
   constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
-  __shared__ int32_t fix_pos[vtx::kCmLoc];  // positions whose raw scores are redone (CMean)
-  __shared__ int fix_n;
 
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
@@ -97,8 +95,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   if (active) {  // uniform
   vtx::select_init<T>(sel, k, sh);
   if constexpr (cm_on) {
-    if (tid == 0) fix_n = 0;
-    __syncthreads();
     closing = vtx::closing_build(cma, cm_pos);
     n_close = closing.count;
   }
@@ -138,9 +134,28 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     }
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
     if (cached && r >= 0) rows[p0 + r] = my_rid;
-    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
-      const int slot = atomicAdd(&fix_n, 1);  // its scores are redone after the loop
-      if (slot < vtx::kCmLoc) fix_pos[slot] = (int32_t)(p0 + r);  // (always, unless a page is listed twice)
+    if constexpr (cm_on) {
+      if (n_close > 0) {  // uniform
+        // pages whose centroid this launch's CMean rewrites: their raw scores
+        // redone against the centroid recomputed from the K tile, one page at
+        // a time per wave, stored by the lane that stored the first ones
+        uint64_t m = __ballot(vtx::closes_here(cma, closing, r, my_rid));
+        while (m) {  // uniform
+          const int l = __ffsll((long long)m) - 1;
+          m &= m - 1;
+          const vtx::U4 cen = vtx::fresh_centroid<LPR>(cma, __builtin_amdgcn_readlane(my_rid, l), grp, col);
+          for (int g = 0; g < G; ++g) {
+            float xg[1][8];
+            vtx::unpack8(vtx::ld16(qs + (long long)g * D + col * 8), xg[0]);
+            const float f = vtx::score_vec<LPR>(cen, xg);
+            if (lane == l) {
+              const uint16_t b = (uint16_t)vtx::f32_to_bf16(f);
+              if (cached) raw[(p0 + r) * G + g] = b;
+              else sc_out[(p0 + r) * G + g] = b;
+            }
+          }
+        }
+      }
     }
   }
   }  // active
@@ -152,29 +167,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     if (!active) return;
   }
   __syncthreads();
-
-  // ---- pages whose centroid this launch's CMean rewrites: their raw scores
-  // against the recomputed centroid, a wave each
-  if constexpr (cm_on) {
-    if (n_close > 0 && fix_n > 0) {  // uniform
-      const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
-      for (int i = wave; i < fixes; i += kWaves) {
-        const int pos = fix_pos[i];
-        const vtx::U4 cen = vtx::fresh_centroid<LPR>(cma, dseg[pos], grp, col);
-        for (int g = 0; g < G; ++g) {
-          float xg[1][8];
-          vtx::unpack8(vtx::ld16(qs + (long long)g * D + col * 8), xg[0]);
-          const float f = vtx::score_vec<LPR>(cen, xg);
-          if (lane == 0) {
-            const uint16_t b = (uint16_t)vtx::f32_to_bf16(f);
-            if (cached) raw[(long long)pos * G + g] = b;
-            else sc_out[(long long)pos * G + g] = b;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
 
   // ---- softmax statistics of each query head over the segment
   auto raw_at = [&](long long i, int g) -> float {

@@ -73,8 +73,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
-  __shared__ int32_t fix_pos[vtx::kCmLoc];  // positions scored after the loop (CMax + CMin)
-  __shared__ int fix_n;
 
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
@@ -106,7 +104,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   int n_close = 0;
   if (active) {  // uniform
   vtx::select_init<T>(sel, k, sh);
-  if (cm_on && tid == 0) fix_n = 0;
   __syncthreads();  // histogram cleared before any wave counts into it
   if constexpr (cm_on) {
     closing = vtx::closing_build(cma, cm_pos);
@@ -148,11 +145,27 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
       }
     }
     const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
-    if (cm_on && n_close > 0 && vtx::closes_here(cma, closing, r, my_rid)) {
-      const int slot = atomicAdd(&fix_n, 1);
-      if (slot < vtx::kCmLoc) {  // its envelopes are rewritten: scored after the loop
-        fix_pos[slot] = (int32_t)(p0 + r);  // (always, unless a page is listed twice)
-        r = -1;
+    if constexpr (cm_on) {
+      if (n_close > 0) {  // uniform
+        // pages whose envelopes this launch rewrites: scored against the
+        // envelopes recomputed from the K tile, one page at a time per wave,
+        // stored by the lane that stored the first scores
+        uint64_t m = __ballot(vtx::closes_here(cma, closing, r, my_rid));
+        while (m) {  // uniform
+          const int l = __ffsll((long long)m) - 1;
+          m &= m - 1;
+          vtx::U4 emx, emn;
+          vtx::fresh_envelope<LPR>(cma, __builtin_amdgcn_readlane(my_rid, l), grp, col, emx, emn);
+          float fbest = -INFINITY;
+          for (int g = 0; g < G; ++g) {
+            float xg[8];
+            vtx::unpack8(vtx::ld16(qs + (long long)g * D + col * 8), xg);
+            const uint32_t b = vtx::f32_to_bf16(quest_vec<LPR>(emx, emn, xg));
+            if (lane == l) a.sum[(start + p0 + r) * G + g] = (uint16_t)b;
+            fbest = fmaxf(fbest, vtx::bf16_to_f32(b));
+          }
+          if (lane == l) best = fbest;
+        }
       }
     }
     if (r >= 0) {
@@ -175,39 +188,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
     if (!active) return;
   }
   __syncthreads();
-
-  // ---- pages whose envelopes this launch rewrites: scored against the
-  // recomputed envelopes, a wave each
-  if constexpr (cm_on) {
-    if (n_close > 0 && fix_n > 0) {  // uniform
-      const int fixes = fix_n < vtx::kCmLoc ? fix_n : vtx::kCmLoc;
-      for (int i = wave; i < fixes; i += kWaves) {
-        const int pos = fix_pos[i];
-        const int rid = dseg[pos];
-        vtx::U4 emx, emn;
-        vtx::fresh_envelope<LPR>(cma, rid, grp, col, emx, emn);
-        float best = -INFINITY;
-        for (int g = 0; g < G; ++g) {
-          float xg[8];
-          vtx::unpack8(vtx::ld16(qs + (long long)g * D + col * 8), xg);
-          const uint32_t b = vtx::f32_to_bf16(quest_vec<LPR>(emx, emn, xg));
-          if (lane == 0) a.sum[(start + pos) * G + g] = (uint16_t)b;
-          best = fmaxf(best, vtx::bf16_to_f32(b));
-        }
-        if (lane == 0) {
-          const uint32_t ab = vtx::f32_to_bf16(best);
-          const uint32_t key = vtx::score_key(ab);
-          a.aggr[start + pos] = (uint16_t)ab;
-          if (cached) {
-            keys[pos] = (uint16_t)key;
-            rows[pos] = rid;
-          }
-          vtx::select_count<T>(key, sh);
-        }
-      }
-      __syncthreads();
-    }
-  }
 
   // ---- top-k of the segment
   if (cached) {
