@@ -163,7 +163,8 @@ class DecodeStep:
         self.cctx.execute()
         self.qmean = torch.empty((B * H, 1, D), device=dev, dtype=torch.bfloat16)
         self.premeaned = None
-        if G > 2:
+        from vortex_torch.indexer.matmul import MEAN_IN_KERNEL_MAX_G
+        if G > MEAN_IN_KERNEL_MAX_G:
             with torch._C.DisableTorchFunctionSubclass():
                 self.premeaned = [qp.mean(dim=1, keepdim=True) for (_, _, qp) in self.plain]
 
@@ -185,7 +186,7 @@ class DecodeStep:
         ic, b = self.ictx, self.batch
         for i, (f, (k, cen, qp)) in enumerate(zip(self.flows, self.plain)):
             with torch._C.DisableTorchFunctionSubclass():
-                if self.premeaned is not None:  # G > 2: the step hands the kernel torch's mean
+                if self.premeaned is not None:  # the step hands the kernel torch's mean
                     q, x_out = self.premeaned[i], None
                 else:
                     q, x_out = qp, self.qmean

@@ -65,10 +65,7 @@ def test_fused_kernel_matches_separate_kernels(gpu, name, mode):
                            seg_counters=counters, mode=mode)
         torch.cuda.synchronize()
         assert int(counters.abs().sum()) == 0, "segment counters not reset"
-    if G <= 2:
-        assert torch.equal(qm, qm_ref), "q-mean differs from torch.mean"
-    else:  # the fp32 sum of G > 2 heads may round differently in another order
-        np.testing.assert_allclose(O.bf16_to_f32(_bits(qm)), O.bf16_to_f32(_bits(qm_ref)), rtol=1e-2, atol=1e-3)
+    assert torch.equal(qm, qm_ref), "q-mean differs from torch.mean"
     # same query -> same scores as the GeMV kernel, written at the same positions
     sc_sep = torch.full_like(sc_ref, -5.0)
     _hip.gemv_paged(qm, y, sc_sep, ic.dense_kv_indices, ic.winfo_q_indices, ic.winfo_kv_offsets,
@@ -78,6 +75,75 @@ def test_fused_kernel_matches_separate_kernels(gpu, name, mode):
     exp, _ = O.topk(_bits(sc), _np(ic.dense_kv_indptr), _np(ic.sparse_kv_indptr), _np(ic.dense_kv_indices),
                     _np(ic.sparse_kv_indices), S, batch.topk, batch.bos, batch.eos)
     np.testing.assert_array_equal(_np(sp), exp)
+
+
+def _wide_q(shape, seed, dev):
+    """bf16 values over 2^-24 .. 2^24: fp32 sums of them round, so a
+    different summation order gives different bits."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    mag = torch.exp2(torch.randint(-24, 24, shape, generator=g, device=dev).float())
+    return (torch.randn(shape, generator=g, device=dev) * mag).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("mode", [_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT])
+@pytest.mark.parametrize("D", [64, 128, 576])
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 6, 8, 12, 16])
+def test_fused_query_mean_is_torch_mean(gpu, G, D, mode):
+    """The kernel's q-mean (written to x_out, also for query rows past the
+    segments) equals torch.mean(dim=1) bit for bit on values whose fp32 sums
+    round: it sums in torch's order and scales by torch's factor."""
+    dev = gpu
+    batch = W.make_batch([4096, 3000, 600], pool_pages=900, seed=40 + G, num_kv_heads=2, group_size=G,
+                         head_dim=D, topk=30, bos=1, eos=1)
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    S = batch.batch * batch.num_kv_heads
+    q = _wide_q((S + 3, G, D), G * 7 + D, dev)
+    y = W.randn_bf16((batch.pool_pages * batch.num_kv_heads, 1, D), 4, dev, std=0.25)
+    qm = torch.full((S + 3, 1, D), 3.0, device=dev, dtype=torch.bfloat16)
+    sc = torch.zeros((ic.dense_kv_indices.numel(), 1, 1), device=dev, dtype=torch.bfloat16)
+    counters = torch.zeros(S, dtype=torch.int32, device=dev)
+    _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices,
+                       ic.sparse_kv_indices.clone(), S, batch.topk, batch.bos, batch.eos,
+                       batch.max_pages_per_request, seg_counters=counters, mode=mode)
+    torch.cuda.synchronize()
+    ref = q.mean(dim=1, keepdim=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_bits(qm), _bits(ref))
+
+
+@pytest.mark.parametrize("cmean", [False, True])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "eos0", "d64", "d256", "d576", "r3", "r9"])
+def test_fused_segment_and_split_layouts_agree(gpu, name, cmean):
+    """FUSED_SEGMENT and FUSED_SPLIT write the same bits: q-mean, scores,
+    block table and (with the layer's CMean) centroids."""
+    dev = gpu
+    batch, loc = W.cmean_case(name)
+    loc = loc.to(dev)
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+    S = batch.batch * H
+    rows = batch.pool_pages * H
+    q = _wide_q((S, G, D), 11, dev)
+    k = W.randn_bf16((rows, P, D), 3, dev)
+    y0 = W.randn_bf16((rows, 1, D), 2, dev, std=0.25)
+    out = {}
+    for mode in (_hip.FUSED_SEGMENT, _hip.FUSED_SPLIT):
+        y = y0.clone()
+        qm = torch.full((S, 1, D), 3.0, device=dev, dtype=torch.bfloat16)
+        sc = torch.full((ic.dense_kv_indices.numel(), 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
+        sp = ic.sparse_kv_indices.clone()
+        counters = torch.zeros(S, dtype=torch.int32, device=dev)
+        _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp, S,
+                           batch.topk, batch.bos, batch.eos, batch.max_pages_per_request, seg_counters=counters,
+                           mode=mode, cmean=(k, loc, H) if cmean else None)
+        torch.cuda.synchronize()
+        out[mode] = (_bits(y), _bits(qm), _bits(sc), _np(sp))
+    for a, b in zip(out[_hip.FUSED_SEGMENT], out[_hip.FUSED_SPLIT]):
+        np.testing.assert_array_equal(a, b)
+    if cmean:
+        assert (out[_hip.FUSED_SPLIT][0] != _bits(y0)).any() or int(((loc + 1) % P == 0).sum()) == 0
 
 
 @pytest.mark.parametrize("kind", ["ties", "const"])
@@ -271,7 +337,8 @@ def _cmean_case(name):
 
 
 @pytest.mark.parametrize("mode", [_hip.FUSED_AUTO, _hip.FUSED_SPLIT])
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "eos0", "mid", "d64", "big_loc", "d256", "r3", "r6", "r9"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "eos0", "mid", "d64", "big_loc", "d256", "d576", "r3", "r6",
+                                  "r9"])
 def test_fused_cmean_equals_separate_launches(gpu, name, mode):
     """vtx_indexer_fused_cmean writes what vtx_page_reduce then
     vtx_indexer_fused write: centroids, q-mean, scores and block table."""

@@ -270,7 +270,11 @@ def cmean_case(name: str):
     if name == "big_loc":  # more loc entries than one launch scans: CMean launched first
         b = make_batch([4096, 4096], pool_pages=600, seed=24)
         return b, torch.arange(300, dtype=torch.int64) * 3
-    if name == "d256":  # wider rows: CMean launched first
+    if name == "d576":  # MLA rows (one latent head of 576), eos 0: closed pages are scored
+        b = make_batch([4096, 5000, 2048, 3072], pool_pages=1200, seed=26, num_kv_heads=1, group_size=16,
+                       head_dim=576, topk=32, bos=1, eos=0)
+        return b, decode_loc(b)
+    if name == "d256":  # wider rows
         b = make_batch([2000, 3000], pool_pages=400, seed=25, head_dim=256, eos=0)
         return b, decode_loc(b)
     if name.startswith("r"):

@@ -47,7 +47,7 @@ namespace {
 struct FusedArgs {
   const uint16_t* q;  // [S, G, D] when G > 0
   int32_t G;
-  float inv_g;        // 1.0f / G
+  float inv_g;        // torch's mean factor (1 / G, as torch rounds it)
   const uint16_t* x;  // [S, D] when G == 0
   uint16_t* x_out;    // q_mean [S, D], optional
   int64_t q_rows;     // S
@@ -67,6 +67,54 @@ struct FusedArgs {
   int32_t segments;  // eff_batch_size; the grid covers all q_rows
   const int32_t* sched;  // the planner's workgroup schedule (vtx_fused_schedule.h), or null
 };
+
+constexpr int kMaxQueryDim = 576;  // the widest supported head_dim
+
+// The bf16 mean of the G query rows at qb ([G, D]) for every column, in
+// torch.mean(dim=1)'s order (its reduction over a strided dimension keeps
+// four fp32 accumulators, row g going to accumulator g % 4 in increasing g,
+// each starting from 0, combined as ((a0 + a1) + a2) + a3, then times the
+// factor inv_g; one thread reduces a whole column up to 16 rows): thread
+// t < D / 8 forms 16-byte column vector t into qm (LDS row of D bf16) and,
+// when `store`, into x_out row `row`.  No barrier.
+__device__ __forceinline__ void query_mean_lds(const FusedArgs& a, const uint16_t* qb, int row, bool store,
+                                               uint16_t* qm) {
+  constexpr int kRowsIn = 8;  // rows loaded before any is added
+  const int D = a.dim;
+  const int nv = D / 8;
+  for (int t = threadIdx.x; t < nv; t += blockDim.x) {
+    float acc[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+    for (int g0 = 0; g0 < a.G; g0 += kRowsIn) {
+      // every load issued before any add (rows past G re-read row G - 1 and
+      // are not added), with constant register indices throughout
+      vtx::U4 r[kRowsIn];
+#pragma unroll
+      for (int j = 0; j < kRowsIn; ++j) {
+        const int g = g0 + j < a.G ? g0 + j : a.G - 1;
+        r[j] = vtx::ld16(qb + (long long)g * D + t * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < kRowsIn; ++j) {
+        if (g0 + j < a.G) {
+          float f[8];
+          vtx::unpack8(r[j], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j % 4][e] += f[e];
+        }
+      }
+    }
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[e] = vtx::f32_to_bf16((((acc[0][e] + acc[1][e]) + acc[2][e]) + acc[3][e]) * a.inv_g);
+    const vtx::U4 m{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+    vtx::st16(qm + t * 8, m);
+    if (store && a.x_out) vtx::st16(a.x_out + (long long)row * D + t * 8, m);
+  }
+}
 
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
 // fp32 mean of its G rows (torch's mean), or the row itself when G == 0.
@@ -154,6 +202,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   constexpr bool kRegSelect = VPL == 1 && (LPR == 8 || LPR == 16) && kPass / kRowsPerLoad == LPR;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
+  __shared__ __align__(16) uint16_t qm_row[VPL * LPR * 8];  // query mean, G > kQRegs
 
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
@@ -296,7 +345,10 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
     }
   }
   if (!active) {
-    if (a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+    if (a.x_out) {
+      if (q_in_regs) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+      else query_mean_lds(a, qb, seg, true, qm_row);
+    }
     cm_tiles();
     return;
   }
@@ -304,8 +356,11 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int32_t* dseg = a.didx + start;
 
   bool have_mean = false;
-  if (!q_in_regs) {  // (more than kQRegs rows to average: before the loop)
-    query_row<LPR, VPL, kQRegs>(a, qv, false, qb, seg, store_mean, col, xs);
+  if (!q_in_regs) {  // (more than kQRegs rows to average: formed in LDS, before the loop)
+    query_mean_lds(a, qb, seg, true, qm_row);
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) vtx::unpack8(vtx::ld16(qm_row + (v * LPR + col) * 8), xs[v]);
     have_mean = true;
   }
 
@@ -419,6 +474,9 @@ __device__ __forceinline__ uint16_t load_coherent(const uint16_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Histogram copies of the split layout's selection (vtx::SelectShared).
+constexpr int kSplitHistCopies = 8;
+
 // Split segments: a segment's middle pages are dealt, kChunk = kWaves * kPass
 // at a time, to `cps` workgroups (chunk c takes chunks c, c + cps, ...).  Each
 // workgroup scores its pages and stores the scores; the one that finishes
@@ -430,15 +488,30 @@ __device__ __forceinline__ uint16_t load_coherent(const uint16_t* p) {
 // Work ids are laid out XCD by XCD (workgroup b runs on XCD b % 8), so the
 // chunks of one segment usually share an L2 and the selecting workgroup reads
 // the other chunks' scores from it.
-template <int T, int LPR, int VPL, int kPass>
-__global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* counters, int32_t cps) {
+//
+// The query mean of more than kQRegs rows is formed once per workgroup in
+// LDS (query_mean_lds).  With kCmRegs > 0 the layer's decode CMean runs in
+// the launch: tile t of the closed pages is reduced by wave t % waves of
+// work id t / waves once that workgroup's scores are counted in, with the
+// page-reduce launch's arithmetic for the row width, and a scored page whose
+// centroid the launch rewrites is scored against the centroid recomputed
+// from its K tile (reduced into the wave's LDS row, read back in the scoring
+// layout).
+template <int T, int LPR, int VPL, int kPass, int kCmRegs>
+__global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* counters, int32_t cps,
+                                                          vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   constexpr int kChunk = kWaves * kPass;
   constexpr int kQRegs = VPL <= 2 ? 2 : 1;
+  constexpr int kTailR = 8;  // scores per thread the selecting workgroup holds in registers
+  constexpr bool cm_on = kCmRegs > 0;
+  constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ vtx::SelectShared<T> sh;
+  __shared__ vtx::SelectShared<T, kSplitHistCopies> sh;
   __shared__ int s_last;
+  __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
+  __shared__ __align__(16) uint16_t fresh_row[cm_on && VPL > 1 ? kWaves * kMaxQueryDim : 8];  // per wave, CMean
 
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
@@ -448,16 +521,36 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   const int k = a.topk;
   const int D = a.dim;
 
+  long long cm_pos[kLocRegs];
+  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
   const long long per_xcd = gridDim.x / 8;  // the host rounds the grid to a multiple of 8
   const long long w = (long long)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   const long long chunk_items = (long long)a.segments * cps;
+  vtx::Closing<kLocRegs> closing{};
+  int n_close = 0;
+  if constexpr (cm_on) {
+    closing = vtx::closing_build(cma, cm_pos);
+    n_close = closing.count;
+  }
+  // this work id's share of the CMean tiles (after its scores are counted in)
+  auto cm_tiles = [&]() {
+    if constexpr (cm_on) {
+      if (w * kWaves < (long long)n_close * cma.heads)  // uniform: tiles w * waves + wave, + grid * waves, ...
+        vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(cma, closing, (int)(w * kWaves) + wave,
+                                                       (int)gridDim.x * kWaves);
+    }
+  };
   float xs[VPL][8];
   vtx::U4 qv[kQRegs][VPL];
   if (w >= chunk_items) {  // query rows past the segments: only their mean
     const long long row = a.segments + (w - chunk_items);
-    if (a.x_out && a.G > 0 && row < a.q_rows)
-      query_row<LPR, VPL, kQRegs>(a, qv, false, a.q + row * a.G * D, (int)row, wave == 0 && grp == 0,
-                                  col, xs);
+    if (a.x_out && a.G > 0 && row < a.q_rows) {
+      if (a.G <= kQRegs)
+        query_row<LPR, VPL, kQRegs>(a, qv, false, a.q + row * a.G * D, (int)row, wave == 0 && grp == 0, col, xs);
+      else
+        query_mean_lds(a, a.q + row * a.G * D, (int)row, true, qm_row);
+    }
+    cm_tiles();
     return;
   }
   const int seg = (int)(w / cps);
@@ -483,14 +576,31 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
     active = false;
   const long long nchunks = active ? (n + kChunk - 1) / kChunk : 0;
   const int workers = (int)min(nchunks, (long long)cps);  // workgroups that take part
+  const bool mean_in_lds = a.G > kQRegs;
   if (c >= workers) {  // nothing to score (or an inactive segment): only the mean
-    if (c == 0 && a.x_out) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+    if (c == 0 && a.x_out) {
+      if (mean_in_lds) query_mean_lds(a, qb, seg, true, qm_row);
+      else query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+    }
+    cm_tiles();
     return;
+  }
+  uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
+  int32_t* sel_pay = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
+  uint16_t* keys = reinterpret_cast<uint16_t*>(sel_pay + k);
+  // the histograms of the final selection are cleared now, off its path (the
+  // barriers of the arrival order this before the counting)
+  vtx::select_init<T>(sel, k, sh);
+  const int32_t* dseg = a.didx + start;
+  if (mean_in_lds) {  // workgroup-uniform
+    query_mean_lds(a, qb, seg, c == 0, qm_row);
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) vtx::unpack8(vtx::ld16(qm_row + (v * LPR + col) * 8), xs[v]);
   }
 
   // ---- scores of this workgroup's chunks
-  const int32_t* dseg = a.didx + start;
-  bool have_mean = false;
+  bool have_mean = mean_in_lds;
   for (long long ch = c; ch < nchunks; ch += cps) {
     const long long c0 = ch * kChunk;
     const long long cn = min((long long)kChunk, n - c0);
@@ -505,16 +615,43 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
       have_mean = true;
     }
     int r;
-    const float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+    float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+    if constexpr (cm_on) {
+      if (n_close > 0) {  // uniform
+        // pages whose centroid this launch's CMean rewrites: scored against
+        // the centroid recomputed from the K tile, one at a time per wave
+        const int my_rid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
+        uint64_t m = __ballot(vtx::closes_here(cma, closing, r, my_rid));
+        while (m) {  // uniform
+          const int l = __ffsll((long long)m) - 1;
+          m &= m - 1;
+          vtx::U4 cen[VPL];
+          vtx::fresh_centroid_rows<LPR, VPL>(cma, __builtin_amdgcn_readlane(my_rid, l),
+                                             fresh_row + wave * kMaxQueryDim, grp, col, cen);
+          const float f = vtx::score_vec_rows<LPR, VPL>(cen, xs);
+          if (lane == l) sc = f;
+        }
+      }
+    }
     if (r >= 0) store_coherent(a.score + start + p0 + r, (uint16_t)vtx::f32_to_bf16(sc));
   }
   // (wave 0 of chunk 0 always has pages, so the mean has been stored)
 
-  // ---- arrival: the last of the `workers` workgroups selects.  The scores
-  // went out as device-coherent stores; each wave waits until its own have
-  // completed, so they are visible to every XCD before the count moves.  No
-  // cache-wide write-back or invalidate is needed on either side.
+  // ---- arrival: the last of the `workers` workgroups selects.  This is a
+  // release/acquire handoff written out for its one kind of payload: the
+  // scores are device-scope atomic stores (written through to the point of
+  // coherence, never held dirty in an XCD's L2), and a release then only
+  // needs each wave to wait until its own stores have completed
+  // (s_waitcnt 0), which happens before the barrier after which one thread
+  // counts the workgroup in with a device-scope atomic.  The last workgroup
+  // reads the scores with device-scope atomic loads issued after that count.
+  // The compiler fences keep the compiler from moving memory operations
+  // across either side.  (A device-scope release fence or release RMW would
+  // also write back the XCD's whole L2 in every workgroup: measured 2.8 to
+  // 5.5 times the launch time at C3 and C5.)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (tid == 0) {
     const int old = __hip_atomic_fetch_add(&counters[seg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -523,14 +660,40 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
     s_last = last;
   }
   __syncthreads();
-  if (!s_last) return;
+  if (!s_last) {
+    cm_tiles();
+    return;
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   // ---- top-k of the segment from the stored scores (device-coherent loads)
-  uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
-  uint16_t* keys = reinterpret_cast<uint16_t*>(smem + (size_t)k * sizeof(uint64_t));
-  const bool cached = n <= a.row_cap;
   const uint16_t* scs = a.score + start;
-  vtx::select_init<T>(sel, k, sh);
+  if (n <= (long long)T * kTailR) {  // uniform: every score and row id in registers
+    // thread t holds positions t * kTailR + u: a thread's items are
+    // consecutive, so one prefix over the lanes ranks the ties
+    bool have[kTailR];
+    uint16_t v[kTailR];
+    int rid[kTailR];
+#pragma unroll
+    for (int u = 0; u < kTailR; ++u) {
+      const long long i = (long long)tid * kTailR + u;
+      have[u] = i < n;
+      v[u] = have[u] ? load_coherent(scs + i) : (uint16_t)0;
+      rid[u] = have[u] ? dseg[i] : -1;
+    }
+    uint32_t key[kTailR];
+#pragma unroll
+    for (int u = 0; u < kTailR; ++u) {
+      key[u] = vtx::score_key(v[u]);
+      if (have[u]) vtx::select_count<T>(key[u], sh);
+    }
+    __syncthreads();
+    vtx::select_regs_run<T, kTailR>(have, key, rid, k, sel, sel_pay, sh,
+                                    [&](int rank, int payload) { a.sidx[obase + rank] = payload; });
+    cm_tiles();
+    return;
+  }
+  const bool cached = n <= a.row_cap;
   __syncthreads();
   // kU loads per thread in flight before any is used
   constexpr int kU = 8;
@@ -559,6 +722,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
                                 sel, sh);
   }
   vtx::select_emit<T>(sel, k, n, [&](int r, long long pos) { a.sidx[obase + r] = dseg[pos]; });
+  cm_tiles();
 }
 
 constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS; the select tables take up to ~6 KB more
@@ -586,8 +750,12 @@ int launch_dim(const FusedArgs& a, const vtx::CmArgs* cm, int blocks, size_t lds
     case 64: indexer_fused_kernel<T, 8, 1, 0><<<blocks, T, lds, s>>>(a, none); break;
     case 128: indexer_fused_kernel<T, 16, 1, 0><<<blocks, T, lds, s>>>(a, none); break;
     case 256: indexer_fused_kernel<T, 16, 2, 0><<<blocks, T, lds, s>>>(a, none); break;
-    case 512: indexer_fused_kernel<T, 16, 4, 0><<<blocks, T, lds, s>>>(a, none); break;
-    case 576: indexer_fused_kernel<T, 8, 9, 0><<<blocks, T, lds, s>>>(a, none); break;
+    case 512:
+      if constexpr (T <= 512) indexer_fused_kernel<T, 16, 4, 0><<<blocks, T, lds, s>>>(a, none);
+      break;
+    case 576:
+      if constexpr (T <= 512) indexer_fused_kernel<T, 8, 9, 0><<<blocks, T, lds, s>>>(a, none);
+      break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_fused");
@@ -600,24 +768,32 @@ constexpr int kSplitThreads = 256;
 int split_pass(int dim) { return dim <= 128 ? 32 : 16; }
 int split_chunk(int dim, bool large) { return (kSplitThreads / 64) * split_pass(dim) * (large ? 2 : 1); }
 
-template <int P>
-int launch_split_pass(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s) {
+template <int P, int kCm>
+int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
+                    const vtx::CmArgs& cm) {
   constexpr int T = kSplitThreads;
   switch (a.dim) {
-    case 64: indexer_split_kernel<T, 8, 1, 2 * P><<<blocks, T, lds, s>>>(a, counters, cps); break;
-    case 128: indexer_split_kernel<T, 16, 1, 2 * P><<<blocks, T, lds, s>>>(a, counters, cps); break;
-    case 256: indexer_split_kernel<T, 16, 2, P><<<blocks, T, lds, s>>>(a, counters, cps); break;
-    case 512: indexer_split_kernel<T, 16, 4, P><<<blocks, T, lds, s>>>(a, counters, cps); break;
-    case 576: indexer_split_kernel<T, 8, 9, P><<<blocks, T, lds, s>>>(a, counters, cps); break;
+    case 64: indexer_split_kernel<T, 8, 1, 2 * P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
+    case 128: indexer_split_kernel<T, 16, 1, 2 * P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
+    case 256: indexer_split_kernel<T, 16, 2, P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
+    case 512: indexer_split_kernel<T, 16, 4, P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
+    case 576: indexer_split_kernel<T, 8, 9, P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
-  return vtx::check_launch("indexer_fused (split)");
+  return vtx::check_launch(kCm ? "indexer_fused (split, with CMean)" : "indexer_fused (split)");
+}
+
+template <int P>
+int launch_split_pass(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
+                      const vtx::CmArgs* cm) {
+  if (cm) return launch_split_cm<P, vtx::kCmLoc / vtx::kWave>(a, counters, cps, blocks, lds, s, *cm);
+  return launch_split_cm<P, 0>(a, counters, cps, blocks, lds, s, vtx::CmArgs{});
 }
 
 int launch_split(const FusedArgs& a, int32_t* counters, int cps, bool large, int blocks, size_t lds,
-                 hipStream_t s) {
-  return large ? launch_split_pass<32>(a, counters, cps, blocks, lds, s)
-               : launch_split_pass<16>(a, counters, cps, blocks, lds, s);
+                 hipStream_t s, const vtx::CmArgs* cm) {
+  return large ? launch_split_pass<32>(a, counters, cps, blocks, lds, s, cm)
+               : launch_split_pass<16>(a, counters, cps, blocks, lds, s, cm);
 }
 
 }  // namespace
@@ -715,7 +891,10 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   FusedArgs a;
   a.q = q;
   a.G = group_size;
-  a.inv_g = group_size > 0 ? 1.0f / (float)group_size : 1.0f;
+  // torch's mean factor: (float)(outputs) / (inputs, converted to float)
+  a.inv_g = group_size > 0 && q_rows > 0
+                ? (float)(q_rows * (long long)head_dim) / (float)(q_rows * (long long)group_size * head_dim)
+                : 1.0f;
   a.x = x;
   a.x_out = group_size > 0 ? x_out : nullptr;
   a.q_rows = q_rows;
@@ -753,10 +932,27 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   // CUs idle, so their pages are split over several workgroups.
   const bool split = mode == VTX_FUSED_SPLIT ||
                      (mode == VTX_FUSED_AUTO && have_counters && (long long)eff_batch_size < 2LL * cus);
-  // The CMean runs inside the segment-layout launch for rows of one 16-byte
-  // vector per lane (its tile layout is then the scoring layout) and decode
-  // sized loc; otherwise as its own launch, first.
-  const bool cm_inside = cms && !split && (head_dim == 64 || head_dim == 128) && cms->nnz <= vtx::kCmLoc;
+  // The CMean runs inside the launch for decode-sized loc and a 16-byte
+  // aligned K pool: in the segment layout for rows of one 16-byte vector per
+  // lane (its tile layout is then the scoring layout), in the split layout
+  // for every supported width; otherwise as its own launch, first.
+  const bool cm_inside = cms && cms->nnz <= vtx::kCmLoc && vtx::aligned16(cms->k) &&
+                         (split || head_dim == 64 || head_dim == 128);
+  vtx::CmArgs cma{};
+  const bool cm_launch = cm_inside && cms->nnz > 0;
+  if (cm_launch) {  // the tiles are spread over the launch's own waves
+    cma.x = cms->k;
+    cma.x_rows = cms->k_rows;
+    cma.rows_per_tile = cms->page_size;
+    cma.cols = head_dim;
+    cma.out = const_cast<uint16_t*>(y);
+    cma.out_rows = y_rows;
+    cma.loc = cms->loc;
+    cma.nnz = cms->nnz;
+    cma.heads = cms->heads;
+    cma.page = cms->page_size;
+  }
+  const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
   if (cms && !cm_inside && cms->nnz > 0) {
     const int rc = vtx_page_reduce(cms->k, cms->k_rows, cms->page_size, head_dim, const_cast<uint16_t*>(y),
                                    VTX_DTYPE_BF16, y_rows, cms->loc, cms->nnz, cms->heads, cms->page_size, 1,
@@ -776,17 +972,17 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     const long long fill = eff_batch_size > 0 ? resident / eff_batch_size : 1;
     if (cps > fill) cps = fill;
     if (cps < 1) cps = 1;
-    const long long room = (kLdsBudget - (long long)a.topk * 8) / 2;
+    const long long room = (kLdsBudget - (long long)a.topk * 12) / 2;
     long long cap = want < room ? want : room;
     cap &= ~7LL;
     if (cap < 0) cap = 0;
     a.row_cap = (int32_t)cap;
-    const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 2;
+    const size_t lds = (size_t)a.topk * 12 + (size_t)cap * 2;  // sel, its payloads, keys
     long long items = (long long)eff_batch_size * cps + (a.x_out ? q_rows - eff_batch_size : 0);
     items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
     if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
     if (items == 0) return VTX_OK;
-    return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s);
+    return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s, cmp);
   }
 
   // the planner's schedule, when it covers this launch's segments
@@ -801,25 +997,12 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   // segments only write their mean).
   const long long grid = a.x_out ? q_rows : eff_batch_size;
   if (grid > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many query rows");
-  vtx::CmArgs cma{};
-  const bool cm_launch = cm_inside && cms->nnz > 0;
-  if (cm_launch) {  // the tiles are spread over the launch's own waves
-    cma.x = cms->k;
-    cma.x_rows = cms->k_rows;
-    cma.rows_per_tile = cms->page_size;
-    cma.cols = head_dim;
-    cma.out = const_cast<uint16_t*>(y);
-    cma.out_rows = y_rows;
-    cma.loc = cms->loc;
-    cma.nnz = cms->nnz;
-    cma.heads = cms->heads;
-    cma.page = cms->page_size;
-  }
   const long long blocks = grid;
   if (blocks == 0) return VTX_OK;
-  const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
   if (max_num_pages <= 256) return launch_dim<256>(a, cmp, (int)blocks, lds, s);
-  if (max_num_pages <= 1024) return launch_dim<512>(a, cmp, (int)blocks, lds, s);
+  // (rows of four or more vectors per lane need more than the 128 registers
+  // a lane of a 1024-thread workgroup can have)
+  if (max_num_pages <= 1024 || head_dim >= 512) return launch_dim<512>(a, cmp, (int)blocks, lds, s);
   return launch_dim<1024>(a, cmp, (int)blocks, lds, s);
 }
 

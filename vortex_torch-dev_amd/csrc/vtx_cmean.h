@@ -154,6 +154,112 @@ __device__ __forceinline__ float score_vec(const U4& cen, const float (&xs)[1][8
   return f;
 }
 
+// Tile `row` reduced with the arithmetic of the page-reduce launch for its
+// width (vtx_page_reduce.h): rows split over 64 / (cols / 8) lane groups and
+// folded across them (reduce_rows_vec_kernel, cols / 8 = 8, 16, 32, 64),
+// else rows summed in order by one lane per 16-byte column vector
+// (reduce_colvec_kernel).  kCentroid: the mean row into dst; kEnvelope: the
+// max row into dst and the min row into dst2 (global or LDS rows of cols
+// bf16).  Wave-level; the tile must be in range.
+template <int LPRT, int kKind>
+__device__ __forceinline__ void tile_reduce_vec(const CmArgs& cm, long long row, uint16_t* dst, uint16_t* dst2) {
+  constexpr int kNeed = kKind == kCentroid ? kNeedSum : (kNeedMax | kNeedMin);
+  const int lane = lane_id();
+  const int grp = lane / LPRT, cv = lane % LPRT;
+  Acc acc[8];
+  tile_stats_vec<LPRT, kNeed>(cm.x, row, cm.rows_per_tile, cm.cols, grp, cv, acc);
+  if (grp == 0) {
+    if constexpr (kKind == kCentroid) {
+      st16(dst + cv * 8, pack_value(acc, VTX_REDUCE_MEAN, cm.rows_per_tile));
+    } else {
+      st16(dst + cv * 8, pack_value(acc, VTX_REDUCE_MAX, cm.rows_per_tile));
+      st16(dst2 + cv * 8, pack_value(acc, VTX_REDUCE_MIN, cm.rows_per_tile));
+    }
+  }
+}
+
+// tile_reduce_vec or the column-vector form, chosen by the row width
+// (kNV = cols / 8 16-byte vectors, a compile-time constant of the caller).
+template <int kNV, int kKind>
+__device__ __forceinline__ void tile_reduce_any(const CmArgs& cm, long long row, uint16_t* dst, uint16_t* dst2) {
+  if constexpr (kNV == 8 || kNV == 16 || kNV == 32 || kNV == 64) {
+    tile_reduce_vec<kNV, kKind>(cm, row, dst, dst2);
+  } else {
+    constexpr int kNeed = kKind == kCentroid ? kNeedSum : (kNeedMax | kNeedMin);
+    constexpr int kRowBatch = 8;
+    const int R = cm.rows_per_tile;
+    constexpr int C = kNV * 8;
+    const uint16_t* tile = cm.x + row * (long long)R * C;
+    for (int cv = lane_id(); cv < kNV; cv += kWave) {
+      Acc acc[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc_init<kNeed>(acc[e]);
+      for (int r0 = 0; r0 < R; r0 += kRowBatch) {
+        U4 v[kRowBatch];
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u)
+          v[u] = r0 + u < R ? ld16_stream(tile + (long long)(r0 + u) * C + cv * 8) : U4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          if (r0 + u >= R) break;
+          float f[8];
+          unpack8(v[u], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc_add<kNeed>(acc[e], f[e]);
+        }
+      }
+      if constexpr (kKind == kCentroid) {
+        st16(dst + cv * 8, pack_value(acc, VTX_REDUCE_MEAN, R));
+      } else {
+        st16(dst + cv * 8, pack_value(acc, VTX_REDUCE_MAX, R));
+        st16(dst2 + cv * 8, pack_value(acc, VTX_REDUCE_MIN, R));
+      }
+    }
+  }
+}
+
+// Tiles first, first + stride, ... of the closed pages reduced as the
+// page-reduce launch for rows of kNV 16-byte vectors would (tile_reduce_any);
+// for kernels whose scoring layout is not the tile layout.  Wave-level.
+template <int kNV, int kLocRegs, int kKind>
+__device__ __forceinline__ void cmean_tiles_any(const CmArgs& cm, const Closing<kLocRegs>& c, int first, int stride) {
+  const int tiles = c.count * cm.heads;
+  for (int t = first; t < tiles; t += stride) {
+    const long long row = (long long)closing_base(c, t / cm.heads) + (t % cm.heads);
+    if (!tile_in_range(cm, row)) continue;
+    tile_reduce_any<kNV, kKind>(cm, row, cm.out + row * cm.cols, cm.out2 ? cm.out2 + row * cm.cols : nullptr);
+  }
+}
+
+// The centroid of tile row `rid` as the CMean launch writes it, delivered in
+// a scoring layout of LPR lanes x VPL 16-byte vectors per row (lane = grp *
+// LPR + col holds vectors v * LPR + col).  One vector per lane: the tile
+// layout is the scoring layout (fresh_centroid).  Wider rows: reduced into
+// the wave's LDS row `scratch` (cols bf16), then read back.  Wave-level.
+template <int LPR, int VPL>
+__device__ __forceinline__ void fresh_centroid_rows(const CmArgs& cm, int rid, uint16_t* scratch, int grp, int col,
+                                                    U4 (&cen)[VPL]) {
+  if constexpr (VPL == 1) {
+    cen[0] = fresh_centroid<LPR>(cm, rid, grp, col);
+  } else {
+    tile_reduce_any<LPR * VPL, kCentroid>(cm, rid, scratch, nullptr);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the row is read by other lanes of the wave
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) cen[v] = ld16(scratch + (v * LPR + col) * 8);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // read before the scratch row is reused
+  }
+}
+
+// score_vec for rows of VPL vectors per lane: the lane's dot_row chain over
+// its vectors, then the xor tree over the LPR lanes (the scoring pass's bits).
+template <int LPR, int VPL>
+__device__ __forceinline__ float score_vec_rows(const U4 (&cen)[VPL], const float (&xs)[VPL][8]) {
+  float f = dot_row<VPL>(cen, xs);
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) f += __shfl_xor(f, d, kWave);
+  return f;
+}
+
 // Whether the lane's pass position (r >= 0, row my_rid) is a tile the
 // in-kernel CMean writes: a row in [page * H, page * H + H) of a closed page,
 // inside the pool and the centroid pool.

@@ -27,14 +27,37 @@ namespace vtx {
 constexpr int kSelU = 4;          // items per thread per round
 constexpr int kSelTieTiles = 64;  // tiles (of T items) with precomputed tie counts
 
-template <int T>
+// The two 256-bin histograms are kept in NC copies (lane l counts into copy
+// l % NC): the keys of one segment share few high bytes, so with one copy
+// most lanes of a wave add to the same LDS word and the atomics serialize.
+// Copies sit kStride words apart (16 bytes of padding shift each copy by four
+// banks).  Readers sum the copies.
+template <int T, int NC = 1>
 struct SelectShared {
-  alignas(16) uint32_t hist[2][256];  // read 16 bytes per lane in sel_find_bin_wave
+  static constexpr int kCopies = NC;
+  static constexpr int kStride = NC > 1 ? 260 : 256;
+  alignas(16) uint32_t hist[2][NC * kStride];  // read 16 bytes per lane in sel_find_bin_wave
   uint32_t wave_ties[T / kWave];
   uint32_t wave_gt[T / kWave];        // select_regs: items above the threshold, per wave
   uint32_t tie_counts[kSelTieTiles * (T / kWave)];  // [tile][wave]
   int count;
 };
+
+// Adds one item to bin `bin` of histogram h (the lane's copy).
+template <int T, int NC>
+__device__ __forceinline__ void sel_hist_add(SelectShared<T, NC>& sh, int h, uint32_t bin) {
+  const int cp = NC > 1 ? (lane_id() % NC) : 0;
+  atomicAdd(&sh.hist[h][cp * SelectShared<T, NC>::kStride + bin], 1u);
+}
+
+// Items in bin `bin` of histogram h (all copies).
+template <int T, int NC>
+__device__ __forceinline__ uint32_t sel_hist_count(const SelectShared<T, NC>& sh, int h, uint32_t bin) {
+  uint32_t c = 0;
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) c += sh.hist[h][cp * SelectShared<T, NC>::kStride + bin];
+  return c;
+}
 
 // Appends this wave's winners (win set) to sel with one LDS atomic for the
 // wave; `comp` is the lane's composite.  Wave-uniform control flow.
@@ -60,10 +83,19 @@ __device__ __forceinline__ long long sel_position(uint64_t c) {
 // (256 bins, higher = better) holding the kt-th best item, i.e.
 // above(b) < kt <= above(b) + hist[b], and above(b) (and hist[b] when
 // `count` is given).
+template <int NC = 1, int kStride = 256>
 __device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t kt, int* bin, int* above,
                                                   int* count = nullptr) {
   const int l = lane_id();
-  const U4 c = ld16(hist + 4 * l);
+  U4 c = ld16(hist + 4 * l);
+#pragma unroll
+  for (int cp = 1; cp < NC; ++cp) {
+    const U4 d = ld16(hist + cp * kStride + 4 * l);
+    c.x += d.x;
+    c.y += d.y;
+    c.z += d.z;
+    c.w += d.w;
+  }
   const uint32_t tot = c.x + c.y + c.z + c.w;
   const uint32_t incl = wave_prefix_sum(tot);
   const uint32_t a3 = lane_value(incl, kWave - 1) - incl;  // items in the bins of higher lanes
@@ -96,11 +128,18 @@ __device__ __forceinline__ void sel_find_bin_wave(const uint32_t* hist, uint32_t
   if (count) *count = m ? (int)lane_value(cb, src) : 0;
 }
 
+// The bin of histogram h holding the kt-th best item (see sel_find_bin_wave).
+template <int T, int NC>
+__device__ __forceinline__ void sel_find_bin(const SelectShared<T, NC>& sh, int h, uint32_t kt, int* bin,
+                                             int* above) {
+  sel_find_bin_wave<NC, SelectShared<T, NC>::kStride>(sh.hist[h], kt, bin, above);
+}
+
 // Clears the histograms, the winner count and the winner slots (no barrier).
-template <int T>
-__device__ __forceinline__ void select_init(uint64_t* sel, int k, SelectShared<T>& sh) {
+template <int T, int NC>
+__device__ __forceinline__ void select_init(uint64_t* sel, int k, SelectShared<T, NC>& sh) {
   const int tid = threadIdx.x;
-  for (int i = tid; i < 256; i += T) {
+  for (int i = tid; i < NC * SelectShared<T, NC>::kStride; i += T) {
     sh.hist[0][i] = 0u;
     sh.hist[1][i] = 0u;
   }
@@ -110,15 +149,15 @@ __device__ __forceinline__ void select_init(uint64_t* sel, int k, SelectShared<T
 
 // Adds one item to the high-byte histogram (callers that produce the keys
 // themselves build it on the fly and then call select_topk_counted).
-template <int T>
-__device__ __forceinline__ void select_count(uint32_t key, SelectShared<T>& sh) {
-  atomicAdd(&sh.hist[0][key >> 8], 1u);
+template <int T, int NC>
+__device__ __forceinline__ void select_count(uint32_t key, SelectShared<T, NC>& sh) {
+  sel_hist_add(sh, 0, key >> 8);
 }
 
 // The selection once hist[0] holds every item (and a barrier made it visible).
-template <int T, typename KeyAt>
+template <int T, int NC, typename KeyAt>
 __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, int k, uint64_t* sel,
-                                                    SelectShared<T>& sh) {
+                                                    SelectShared<T, NC>& sh) {
   constexpr int kWaves = T / kWave;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -127,7 +166,7 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
   // Every wave reads the threshold bins off the LDS histograms itself, so
   // no barrier is needed to broadcast them.
   int hi_bin = 0, above_hi = 0;
-  sel_find_bin_wave(sh.hist[0], (uint32_t)k, &hi_bin, &above_hi);
+  sel_find_bin(sh, 0, (uint32_t)k, &hi_bin, &above_hi);
   const uint32_t hi = (uint32_t)hi_bin;
 
   // kSelU keys per thread per round, their reads issued together; the keys
@@ -143,7 +182,7 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
 #pragma unroll
     for (int u = 0; u < kSelU; ++u) {
       const long long i = i0 + (long long)u * T + tid;
-      if (i < n && (key[u] >> 8) == hi) atomicAdd(&sh.hist[1][key[u] & 255u], 1u);
+      if (i < n && (key[u] >> 8) == hi) sel_hist_add(sh, 1, key[u] & 255u);
     }
   };
   uint32_t key0[kSelU];
@@ -156,10 +195,10 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
   }
   __syncthreads();
   int lo_bin = 0, above_lo = 0;
-  sel_find_bin_wave(sh.hist[1], (uint32_t)(k - above_hi), &lo_bin, &above_lo);
+  sel_find_bin(sh, 1, (uint32_t)(k - above_hi), &lo_bin, &above_lo);
   const uint32_t thr = (hi << 8) | (uint32_t)lo_bin;
   const int take = k - (above_hi + above_lo);  // >= 1 items equal to thr win
-  const bool all_ties = (take == (int)sh.hist[1][thr & 255u]);
+  const bool all_ties = (take == (int)sel_hist_count(sh, 1, thr & 255u));
   const long long tiles = (n + T - 1) / T;
   const bool tie_table = !all_ties && tiles <= kSelTieTiles;
 
@@ -236,9 +275,9 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
 }
 
 // key_at(i) returns the order key of item i < n.  Requires 0 < k < n.
-template <int T, typename KeyAt>
+template <int T, int NC, typename KeyAt>
 __device__ __forceinline__ void select_topk(KeyAt key_at, long long n, int k, uint64_t* sel,
-                                            SelectShared<T>& sh) {
+                                            SelectShared<T, NC>& sh) {
   select_init<T>(sel, k, sh);
   __syncthreads();
   for (long long i = threadIdx.x; i < n; i += T) select_count<T>(key_at(i), sh);
@@ -312,19 +351,19 @@ __device__ __forceinline__ int pass_rank_below(uint64_t m) {
 // emit(rank, payload) is called once per winner.  sel holds k composites,
 // sel_pay k payloads (LDS, 16-byte aligned).  Requires 0 < k < n; every
 // thread of the workgroup calls it (it contains barriers).
-template <int T, int LPR, typename Emit>
+template <int T, int LPR, int NC, typename Emit>
 __device__ __forceinline__ void select_regs(bool have, uint32_t key, long long pos, int payload, int k,
-                                            uint64_t* sel, int32_t* sel_pay, SelectShared<T>& sh, Emit emit) {
+                                            uint64_t* sel, int32_t* sel_pay, SelectShared<T, NC>& sh, Emit emit) {
   constexpr int kWaves = T / kWave;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = uniform(tid / kWave);
   int hi = 0, above_hi = 0;
-  sel_find_bin_wave(sh.hist[0], (uint32_t)k, &hi, &above_hi);
-  if (have && (key >> 8) == (uint32_t)hi) atomicAdd(&sh.hist[1][key & 255u], 1u);
+  sel_find_bin(sh, 0, (uint32_t)k, &hi, &above_hi);
+  if (have && (key >> 8) == (uint32_t)hi) sel_hist_add(sh, 1, key & 255u);
   __syncthreads();
   int lo = 0, above_lo = 0;
-  sel_find_bin_wave(sh.hist[1], (uint32_t)(k - above_hi), &lo, &above_lo);
+  sel_find_bin(sh, 1, (uint32_t)(k - above_hi), &lo, &above_lo);
   const uint32_t thr = ((uint32_t)hi << 8) | (uint32_t)lo;
   const int above = above_hi + above_lo;  // items with a key above thr
   const int take = k - above;             // >= 1 of the items equal to thr win
@@ -351,6 +390,73 @@ __device__ __forceinline__ void select_regs(bool have, uint32_t key, long long p
   if (win) {
     sel[slot] = sel_composite(key, pos);
     sel_pay[slot] = payload;
+  }
+  __syncthreads();
+  for (int j = tid; j < k; j += T) {
+    const uint64_t c = sel[j];
+    emit(rank_of_pairs(c, sel, k), sel_pay[j]);
+  }
+}
+
+// select_regs for kR items per thread at consecutive positions: item u of
+// thread tid is at position tid * kR + u (have[u], key[u], payload[u]).
+// hist[0] must hold the high-byte counts of every item and hist[1] zeros,
+// visible after a barrier.  A thread's count of items above and equal to the
+// threshold, an inclusive scan over the wave's lanes and one LDS exchange of
+// the wave totals give every item its winner slot.  emit(rank, payload) is
+// called once per winner.  Requires 0 < k < n; every thread of the
+// workgroup calls it.
+template <int T, int kR, int NC, typename Emit>
+__device__ __forceinline__ void select_regs_run(const bool (&have)[kR], const uint32_t (&key)[kR],
+                                                const int (&payload)[kR], int k, uint64_t* sel, int32_t* sel_pay,
+                                                SelectShared<T, NC>& sh, Emit emit) {
+  constexpr int kWaves = T / kWave;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid / kWave);
+  int hi = 0, above_hi = 0;
+  sel_find_bin(sh, 0, (uint32_t)k, &hi, &above_hi);
+#pragma unroll
+  for (int u = 0; u < kR; ++u)
+    if (have[u] && (key[u] >> 8) == (uint32_t)hi) sel_hist_add(sh, 1, key[u] & 255u);
+  __syncthreads();
+  int lo = 0, above_lo = 0;
+  sel_find_bin(sh, 1, (uint32_t)(k - above_hi), &lo, &above_lo);
+  const uint32_t thr = ((uint32_t)hi << 8) | (uint32_t)lo;
+  const int above = above_hi + above_lo;  // items with a key above thr
+  const int take = k - above;             // >= 1 of the items equal to thr win
+  uint32_t n_gt = 0, n_tie = 0;
+#pragma unroll
+  for (int u = 0; u < kR; ++u) {
+    n_gt += (have[u] && key[u] > thr) ? 1u : 0u;
+    n_tie += (have[u] && key[u] == thr) ? 1u : 0u;
+  }
+  const uint32_t gt_incl = wave_prefix_sum(n_gt);
+  const uint32_t tie_incl = wave_prefix_sum(n_tie);
+  if (lane == kWave - 1) {
+    sh.wave_gt[wave] = gt_incl;
+    sh.wave_ties[wave] = tie_incl;
+  }
+  __syncthreads();
+  int gt_slot = (int)(gt_incl - n_gt), tie_rank = (int)(tie_incl - n_tie);
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) {
+      gt_slot += (int)sh.wave_gt[w];
+      tie_rank += (int)sh.wave_ties[w];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kR; ++u) {
+    const bool gt = have[u] && key[u] > thr;
+    const bool tie = have[u] && key[u] == thr;
+    if (gt || (tie && tie_rank < take)) {
+      const int slot = gt ? gt_slot : above + tie_rank;
+      sel[slot] = sel_composite(key[u], (long long)tid * kR + u);
+      sel_pay[slot] = payload[u];
+    }
+    gt_slot += gt ? 1 : 0;
+    tie_rank += tie ? 1 : 0;
   }
   __syncthreads();
   for (int j = tid; j < k; j += T) {

@@ -25,6 +25,10 @@ from . import _walk
 from .context import Context
 
 
+#: Largest query group the fused kernel averages itself (torch.mean's order).
+MEAN_IN_KERNEL_MAX_G = 16
+
+
 class PendingGemv(_deferred.Pending):
     """A recorded ``GeMV`` launch.  ``topK`` on its result replaces it (and
     the recorded mean of its query, if any) by one fused launch."""
@@ -50,10 +54,11 @@ class PendingGemv(_deferred.Pending):
                 if p is mean or p is self:
                     break
                 p.flush()
-        # The kernel folds the mean in when its fp32 sum cannot differ from
-        # torch's (at most two query heads per kv head); otherwise torch's
-        # mean runs first and the kernel starts from its result.
-        if isinstance(mean, _deferred.PendingMean) and int(mean.q.shape[1]) <= 2:
+        # The kernel folds the mean in with torch's summation order, which
+        # torch keeps for up to 16 query heads per kv head (four fp32
+        # accumulators over the heads, one thread per column); past that
+        # torch's mean runs first and the kernel starts from its result.
+        if isinstance(mean, _deferred.PendingMean) and int(mean.q.shape[1]) <= MEAN_IN_KERNEL_MAX_G:
             q, x_out = mean.q, mean.out
         else:
             _deferred.materialize(self.x)
