@@ -225,6 +225,28 @@ int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                       int32_t* seg_counters, int64_t seg_counters_len, int32_t mode,
                       const int32_t* schedule, int64_t schedule_len, void* stream);
 
+/*
+ * vtx_indexer_fused without the seg_counters workspace: the split layout's
+ * per-segment arrival counters live in a device array of the library
+ * (65,536 int32 per device, held until the process ends), so the call
+ * allocates nothing and takes no workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The
+ * first call on a device looks the array up and clears it (a fill kernel on
+ * `stream`).  At most 65,536 segments (eff_batch_size), else VTX_E_INVALID.
+ * Every call on a device shares the array: calls that overlap on one device
+ * (other streams, other threads) race and must be serialized by the caller.
+ */
+int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                              const uint16_t* x, uint16_t* x_out, const uint16_t* y,
+                              int64_t y_rows, uint16_t* score, int64_t score_len,
+                              const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                              const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                              int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                              int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                              int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
+                              int32_t mode, const int32_t* schedule, int64_t schedule_len, void* stream);
+
 /* 1 if vtx_indexer_fused handles this head_dim (64, 128, 256, 512, 576). */
 int vtx_indexer_fused_supported(int32_t head_dim);
 

@@ -1007,3 +1007,74 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
 }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// vtx_indexer_fused_noalloc: vtx_indexer_fused with the split layout's
+// per-segment arrival counters in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate.  Every device keeps its
+// own copy of the array until the process ends; the kernels take its device
+// address (queried once per device with that device current), never the
+// host-side name.  Each launch leaves every counter it used at zero, so the
+// array only needs clearing once, by a fill kernel on the first call's
+// stream.  Calls that overlap on one device share the counters and race.
+#include <mutex>
+
+namespace {
+
+constexpr int64_t kStaticCounters = 65536;  // segments a no-allocation call may have
+static __device__ __align__(256) int32_t scratch[kStaticCounters];
+
+__global__ void clear_counters_kernel(int32_t* c, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    c[i] = 0;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// This device's counters (set up on the first call on the device).
+int static_counters(hipStream_t s, int32_t** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return vtx::fail(VTX_E_DEVICE, "indexer_fused_noalloc: no usable current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return vtx::fail(VTX_E_DEVICE, "indexer_fused_noalloc: cannot get the counters' address: %s",
+                       hipGetErrorString(e));
+    clear_counters_kernel<<<64, 256, 0, s>>>(static_cast<int32_t*>(p), kStaticCounters);
+    const int rc = vtx::check_launch("indexer_fused_noalloc (clearing the counters)");
+    if (rc != VTX_OK) return rc;
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return VTX_OK;
+}
+
+}  // namespace
+
+extern "C" int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int32_t group_size,
+                                         const uint16_t* x, uint16_t* x_out, const uint16_t* y,
+                                         int64_t y_rows, uint16_t* score, int64_t score_len,
+                                         const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr,
+                                         const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
+                                         int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
+                                         int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
+                                         int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
+                                         int32_t mode, const int32_t* schedule, int64_t schedule_len,
+                                         void* stream) {
+  vtx::clear_error();
+  if (eff_batch_size > kStaticCounters)
+    return vtx::fail(VTX_E_INVALID, "indexer_fused_noalloc: %d segments exceed the %lld it serves",
+                     eff_batch_size, (long long)kStaticCounters);
+  int32_t* counters = nullptr;
+  const int rc = static_counters(vtx::as_stream(stream), &counters);
+  if (rc != VTX_OK) return rc;
+  return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
+                    sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
+                    sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
+                    head_dim, counters, kStaticCounters, mode, nullptr, schedule, schedule_len, stream);
+}

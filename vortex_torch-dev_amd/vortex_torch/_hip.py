@@ -60,6 +60,11 @@ _SIGNATURES = {
          _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _vp, _i64, _vp],
         ctypes.c_int,
     ),
+    "vtx_indexer_fused_noalloc": (
+        [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
+         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
+        ctypes.c_int,
+    ),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
     "vtx_indexer_fused_cmean": (
         [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
@@ -572,6 +577,7 @@ def indexer_fused(
     mode: int = FUSED_AUTO,
     cmean=None,
     schedule=None,
+    noalloc: bool = False,
 ) -> None:
     """q-mean + GeMV + topK of one layer in one launch.
 
@@ -586,7 +592,9 @@ def indexer_fused(
     the same launch (``vtx_indexer_fused_cmean``), with the results of a
     separate ``page_reduce`` launch before this one.  schedule: the
     fused_schedule plan_decode wrote for this block table (the workgroup
-    order of the one-workgroup-per-segment layout; speed only).
+    order of the one-workgroup-per-segment layout; speed only).  noalloc:
+    launch through ``vtx_indexer_fused_noalloc`` (the library's own
+    counters; no seg_counters, no cmean).
     """
     lib = load_library()
     tensors = [q, y, score, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
@@ -635,6 +643,13 @@ def indexer_fused(
     if schedule is not None:
         _req(schedule, torch.int32, "schedule")
     sched = (schedule.data_ptr() if schedule is not None else None, schedule.numel() if schedule is not None else 0)
+    if noalloc:
+        if seg_counters is not None or cmean is not None:
+            raise RuntimeError("vortex_torch: the no-allocation entry point takes no seg_counters and no cmean")
+        with _on_device(dev):
+            rc = lib.vtx_indexer_fused_noalloc(*args[:-3], int(mode), *sched, _stream(dev))
+        _check(rc, "indexer_fused_noalloc")
+        return
     if cmean is not None:
         k, loc, heads = cmean
         _req(k, torch.bfloat16, "k_cache")
