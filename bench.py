@@ -7,33 +7,36 @@ close) and forward_indexer (q head-group mean, GeMV, topK) — for batch 64,
 L ~ U[1024, 8192], page 16, top-30 + 1 BOS + 1 EOS.  Every layer has its own
 centroid pool and K pool (together far larger than the 256 MB Infinity
 Cache, so replays do not hit in it).  The step is captured once as a HIP
-graph and replayed; `value` is µs per step (HIP events on the replay stream).
+graph; `--steps` replays are timed one by one with HIP events on the replay
+stream and `value` is their median in µs (min, max and mean in replay_us).
 
 Extra fields: achieved_GBps (algorithmic bytes of the step / time); roofline
 (the fused indexer kernel — the dominant one — timed alone from a graph of
-its 27 per-layer launches); unfused_us_per_step (the same step with every op
-launched separately, VORTEX_FUSE=0); cpu_baseline (the CPU oracle on a
-bounded sample of the same step).
+its 27 per-layer launches, at least 50 replays, median per launch);
+unfused_us_per_step (the same step with every op launched separately,
+VORTEX_FUSE=0); cpu_baseline (the CPU oracle on the same step, one thread
+per host core, median of 3 runs); configs (C3, C4 and C5 measured the same
+way: their step, or C4's burst, and their dominant kernel's roofline).
 
-Other configurations (side measurements, not the headline):
-  --config c3 / c5   the same decode step at C3 (8 x 32k tokens, top-64) or C5
-                     (MLA latent cache, D 576, G 16, top-32) shape;
+Other invocations:
+  --config c3 / c5   a line for the C3 (8 x 32k tokens, top-64) or C5 (MLA
+                     latent cache, D 576, G 16, top-32) decode step;
   --config c4        page-finish burst: CMean + CMax of 65,536 pages (1M loc
                      entries) into a 70k-page pool, fused (one pass over K)
                      and as two separate ops.
-  --traffic-probe    launches the fused indexer kernel of every layer eagerly,
-                     then a bf16 negation of a 512 MiB buffer (a copy kernel of
-                     known size), and exits: the program a counter pass
-                     (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) profiles.
-
+  --traffic-probe    launches the fused indexer kernel of every layer eagerly
+                     (with --probe-unfused also the step with every op on its
+                     own; at C4 the burst), then a bf16 negation of a 512 MiB
+                     buffer (a copy kernel of known size), and exits: the
+                     program the counter passes (rocprofv3 --pmc) profile.
   --attention        paged decode attention over the sparse table the indexer
                      selects and over the dense table (all pages), per layer;
   --flow gqa / quest the same decode step with gqa_block_sparse_attention or
-                     gqa_quest_sparse_attention (every op launched on its own).
+                     gqa_quest_sparse_attention.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
                        [--config c2|c3|c4|c5] [--flow block_sparse|gqa|quest] [--attention]
-                       [--layers N] [--traffic-probe]
+                       [--layers N] [--traffic-probe [--probe-unfused]]
 """
 from __future__ import annotations
 
@@ -80,6 +83,9 @@ def _parse():
                     help="side measurement: paged decode attention over the sparse and the dense table")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the kernels a counter pass profiles, print their sizes, exit")
+    ap.add_argument("--probe-unfused", action="store_true",
+                    help="with --traffic-probe: also run the step with every op launched on its own")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C3 / C4 / C5 keys of the C2 line")
     return ap.parse_args()
 
 
@@ -110,7 +116,8 @@ def fused_kernel_name(batch: W.DecodeBatch) -> str:
         small_pass = 32 if batch.head_dim <= 128 else 16
         mid = max(1, batch.max_pages_per_request - batch.bos - batch.eos)
         large = segments * -(-mid // (4 * small_pass)) > 4 * cus
-        return f"indexer_split_kernel<256, {lpr}, {vpl}, {small_pass * (2 if large else 1)}>"
+        cm = 4 if batch.batch <= 256 else 0  # the decode CMean in the launch (loc in four registers per lane)
+        return f"indexer_split_kernel<256, {lpr}, {vpl}, {small_pass * (2 if large else 1)}, {cm}>"
     mp = batch.max_pages_per_request
     T = 256 if mp <= 256 else (512 if mp <= 1024 else 1024)
     # the decode CMean (loc: one token per request) runs in the same launch
@@ -212,9 +219,10 @@ def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: n
     # topK: score + row id per candidate page, top-k ids written
     topk = covered * (2 + 4) + sel_segs * batch.topk * 4
     qmean = q_in + q_out
-    # fused kernel: query in (the G heads, or torch's mean when G > 2), mean out
-    # (G <= 2), row ids + centroid rows in, scores out, ids out
-    fused_q = q_in + q_out if G <= 2 else q_out
+    # fused kernel: query in (the G heads, or torch's mean past 16 heads), mean
+    # out, row ids + centroid rows in, scores out, ids out
+    from vortex_torch.indexer.matmul import MEAN_IN_KERNEL_MAX_G
+    fused_q = q_in + q_out if G <= MEAN_IN_KERNEL_MAX_G else q_out
     ndense = int(dip[-1])
     plan_b = ndense * 4 + (ndense // H) * 4 + 2 * (B * H + 1) * 4 + int(plan["sparse_indptr"][-1]) * 4 + B * 16
     finishing = int(((loc_host + 1) % P == 0).sum()) * H
@@ -228,20 +236,33 @@ def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: n
             "step": plan_b + layers * per_layer, "covered_pages": covered}
 
 
-def time_graph(graph: torch.cuda.CUDAGraph, reps: int, warmup: int) -> float:
-    """Mean milliseconds per replay; replays and events on the current stream."""
+def time_replays(graph: torch.cuda.CUDAGraph, reps: int, warmup: int) -> np.ndarray:
+    """Milliseconds of each of `reps` back-to-back replays: a HIP event is
+    recorded on the replay stream before the first replay and after every
+    replay, so replay i is the interval between events i and i + 1."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for _ in range(reps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record(stream)
+    for i in range(reps):
         graph.replay()
-    t1.record(stream)
-    t1.synchronize()
-    return t0.elapsed_time(t1) / reps
+        ev[i + 1].record(stream)
+    ev[-1].synchronize()
+    return np.array([ev[i].elapsed_time(ev[i + 1]) for i in range(reps)])
+
+
+def time_graph(graph: torch.cuda.CUDAGraph, reps: int, warmup: int) -> float:
+    """Median milliseconds per replay (see time_replays)."""
+    return float(np.median(time_replays(graph, reps, warmup)))
+
+
+def replay_stats(ms: np.ndarray, per: float = 1.0) -> dict:
+    """Median, min, max and mean in µs of per-replay times, divided by `per`."""
+    us = ms * 1000.0 / per
+    return {"median": round(float(np.median(us)), 3), "min": round(float(us.min()), 3),
+            "max": round(float(us.max()), 3), "mean": round(float(us.mean()), 3), "n": int(us.size)}
 
 
 def capture(fn) -> torch.cuda.CUDAGraph:
@@ -257,9 +278,14 @@ def capture(fn) -> torch.cuda.CUDAGraph:
     return g
 
 
-def cpu_baseline(batch: W.DecodeBatch, step: DecodeStep, sample_layers: int = 8) -> dict:
-    """The CPU oracle (numpy, one thread) on the same data: plan + `sample_layers`
-    layers of (CMean of closed pages, q-mean, GeMV, topK), scaled to the step."""
+def cpu_baseline(batch: W.DecodeBatch, step: DecodeStep, reps: int = 3) -> dict:
+    """The CPU oracle (numpy) on the same data: the whole step — plan, then
+    for every layer the CMean of the closed pages, q-mean, GeMV and topK —
+    with the layers spread over one thread per host core the process may
+    use (numpy's own thread pools held to one thread each), `reps` times;
+    the median wall time is reported."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from threadpoolctl import threadpool_limits
 
     from oracle import vortex_oracle as O
@@ -269,33 +295,36 @@ def cpu_baseline(batch: W.DecodeBatch, step: DecodeStep, sample_layers: int = 8)
 
     H, D, P = batch.num_kv_heads, batch.head_dim, batch.page_size
     sl, r2t, ri = batch.seq_lens.numpy(), batch.req_to_token.numpy(), batch.req_indices.numpy()
-    n_layers = min(sample_layers, step.layers)
-    with threadpool_limits(limits=1):
-        t0 = time.perf_counter()
-        plan = O.plan_decode(sl, r2t, ri, P, H, batch.topk, batch.bos, batch.eos, batch.max_chunk)
-        t_plan = time.perf_counter() - t0
-        t_layers = 0.0
-        for layer in range(n_layers):
-            k_pool, cen_pool, q_plain = step.plain[layer]
-            trig = step.loc_host[(step.loc_host + 1) % P == 0]
-            rows = np.unique((trig[:, None] // P * H + np.arange(H)[None, :]).reshape(-1))
-            k_rows = bits(k_pool[torch.as_tensor(rows, device=step.dev)]) if rows.size else np.zeros((0, P, D), np.uint16)
-            cen, q = bits(cen_pool), bits(q_plain)
+    cores = len(os.sched_getaffinity(0))
+    trig = step.loc_host[(step.loc_host + 1) % P == 0]
+    rows = np.unique((trig[:, None] // P * H + np.arange(H)[None, :]).reshape(-1))
+    host = []  # each layer's inputs on the host (copied before the timed region)
+    for k_pool, cen_pool, q_plain in step.plain:
+        k_rows = bits(k_pool[torch.as_tensor(rows, device=step.dev)]) if rows.size else np.zeros((0, P, D), np.uint16)
+        host.append((k_rows, bits(cen_pool), bits(q_plain)))
+
+    def layer(plan, i):
+        k_rows, cen, q = host[i]
+        # CMean of the closed pages; the compact copy holds page i at rows i*H..i*H+H-1
+        O.page_reduce(k_rows, np.zeros((rows.size, 1, D), np.uint16),
+                      np.arange(0, rows.size // H) * P + (P - 1), H, P, 1, O.MEAN)
+        qm = O.q_group_mean(q)
+        sc, _ = O.gemv(qm, cen, plan["dense_indices"], plan["winfo_q"], plan["winfo_off"], plan["winfo_len"],
+                       plan["num_workloads"], int(plan["dense_indptr"][-1]))
+        O.topk(sc, plan["dense_indptr"], plan["sparse_indptr"], plan["dense_indices"], plan["sparse_indices"],
+               batch.batch * H, batch.topk, batch.bos, batch.eos)
+
+    times = []
+    with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=cores) as pool:
+        for _ in range(reps):
             t0 = time.perf_counter()
-            # CMean of the closed pages; the compact copy holds page i at rows i*H..i*H+H-1
-            O.page_reduce(k_rows, np.zeros((rows.size, 1, D), np.uint16),
-                          np.arange(0, rows.size // H) * P + (P - 1), H, P, 1, O.MEAN)
-            qm = O.q_group_mean(q)
-            sc, _ = O.gemv(qm, cen, plan["dense_indices"], plan["winfo_q"], plan["winfo_off"],
-                           plan["winfo_len"], plan["num_workloads"], int(plan["dense_indptr"][-1]))
-            O.topk(sc, plan["dense_indptr"], plan["sparse_indptr"], plan["dense_indices"],
-                   plan["sparse_indices"], batch.batch * H, batch.topk, batch.bos, batch.eos)
-            t_layers += time.perf_counter() - t0
-    per_step = t_plan + t_layers * step.layers / n_layers
-    return {"value": round(per_step * 1e6, 1), "unit": "us/step", "cores": 1, "kind": "port",
-            "sample": f"plan + {n_layers} of {step.layers} layers of the same step (oracle, numpy, "
-                      f"1 thread), layer time scaled to {step.layers} layers; measured "
-                      f"{t_plan + t_layers:.2f} s"}
+            plan = O.plan_decode(sl, r2t, ri, P, H, batch.topk, batch.bos, batch.eos, batch.max_chunk)
+            list(pool.map(lambda i: layer(plan, i), range(len(host))))
+            times.append(time.perf_counter() - t0)
+    return {"value": round(float(np.median(times)) * 1e6, 1), "unit": "us/step", "cores": cores, "kind": "port",
+            "sample": f"the whole step (plan + {len(host)} layers) of the same data, layers spread over "
+                      f"{cores} threads (one per host core of the process), median of {reps} runs: "
+                      + ", ".join(f"{t:.2f} s" for t in times)}
 
 
 def plan_summary(step: DecodeStep) -> dict:
@@ -312,79 +341,114 @@ def plan_summary(step: DecodeStep) -> dict:
         }
 
 
-def bench_decode(args, dev) -> dict:
-    batch = getattr(W, args.config)()
-    print(f"[bench] building {args.config.upper()} step: {batch.batch} requests, {args.layers} layers",
+def measure_decode(cfg: str, args, dev, unfused: bool = False, cpu: bool = False) -> dict:
+    """One decode configuration: the step graph (args.steps replays, each
+    timed), the fused indexer kernel of every layer from a graph of its
+    launches (at least 50 replays, each timed), their algorithmic bytes, and
+    optionally the unfused step and the CPU baseline."""
+    import gc
+
+    batch = getattr(W, cfg)()
+    print(f"[bench] building {cfg.upper()} step: {batch.batch} requests, {args.layers} layers",
           file=sys.stderr, flush=True)
     step = DecodeStep(batch, args.layers, dev)
-
-    if args.traffic_probe:
-        return traffic_probe(step, dev)
-
     os.environ["VORTEX_FUSE"] = "1"
     g = capture(step.run)
-    us_step = time_graph(g, args.steps, args.warmup) * 1000.0
-    print(f"[bench] step {us_step:.1f} us", file=sys.stderr, flush=True)
+    step_ms = time_replays(g, args.steps, args.warmup)
+    del g
+    st = replay_stats(step_ms)
+    print(f"[bench] {cfg} step {st['median']:.1f} us (min {st['min']:.1f}, max {st['max']:.1f})",
+          file=sys.stderr, flush=True)
     plan = plan_summary(step)
     nbytes = algorithmic_bytes(batch, plan, args.layers, step.loc_host)
 
     gk = capture(step.indexer_kernels_only)
-    us_fused = time_graph(gk, args.kernel_reps, 3) * 1000.0 / args.layers
+    kern = replay_stats(time_replays(gk, max(50, args.kernel_reps), 3), per=args.layers)
+    del gk
+    us_fused = kern["median"]
     fused_gbps = nbytes["fused"] / (us_fused * 1e-6) / 1e9
-    print(f"[bench] fused indexer {us_fused:.2f} us/launch, {fused_gbps:.0f} GB/s", file=sys.stderr, flush=True)
-
-    unfused = None
-    if not args.no_unfused:
+    print(f"[bench] {cfg} fused indexer {us_fused:.2f} us/launch, {fused_gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    res = {
+        "workload": DECODE_CONFIGS[cfg],
+        "us_per_step": st,
+        "batch": batch.batch,
+        "layers": args.layers,
+        "dense_pages": int(plan["dense_indptr"][-1]),
+        "scored_pages_per_layer": nbytes["covered_pages"],
+        "max_chunk_size": batch.max_chunk,
+        "algorithmic_bytes_per_step": nbytes["step"],
+        "achieved_GBps": round(nbytes["step"] / (st["median"] * 1e-6) / 1e9, 1),
+        "roofline": {
+            "kernel": f"{fused_kernel_name(batch)} (CMean of the closed pages + q-mean + GeMV + top-k, one layer)",
+            "bound": "hbm",
+            "achieved": round(fused_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(fused_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(cfg),
+            "us_per_launch": us_fused,
+            "us_per_launch_stats": kern,
+            "bytes_per_launch": nbytes["fused"],
+        },
+    }
+    if unfused:
         os.environ["VORTEX_FUSE"] = "0"
         gu = capture(step.run)
-        unfused = round(time_graph(gu, max(5, args.steps // 5), 3) * 1000.0, 2)
+        res["unfused_us_per_step"] = replay_stats(time_replays(gu, max(10, args.steps // 5), 3))["median"]
         os.environ["VORTEX_FUSE"] = "1"
         del gu
-        print(f"[bench] unfused step {unfused:.1f} us", file=sys.stderr, flush=True)
+        print(f"[bench] {cfg} unfused step {res['unfused_us_per_step']:.1f} us", file=sys.stderr, flush=True)
+    if cpu:
+        print("[bench] cpu baseline (oracle)", file=sys.stderr, flush=True)
+        res["cpu_baseline"] = cpu_baseline(batch, step)
+    del step
+    gc.collect()
+    torch.cuda.empty_cache()
+    return res
 
-    gbps = nbytes["step"] / (us_step * 1e-6) / 1e9
-    kernel = fused_kernel_name(batch)
+
+def bench_decode(args, dev) -> dict:
+    if args.traffic_probe:
+        batch = getattr(W, args.config)()
+        return traffic_probe(DecodeStep(batch, args.layers, dev), dev, unfused=args.probe_unfused)
+    m = measure_decode(args.config, args, dev, unfused=not args.no_unfused, cpu=not args.no_cpu)
+    st = m["us_per_step"]
     out = {
         "metric": METRIC,
-        "value": round(us_step, 2),
+        "value": st["median"],
         "unit": "us/step",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(us_step / 1000.0, 4),
+        "ms_per_step": round(st["median"] / 1000.0, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": f"synthetic (seeded; random-init K, centroid and query tensors of the "
                 f"{args.config.upper()} shapes)",
-        "config": {
-            "workload": DECODE_CONFIGS[args.config],
-            "batch": batch.batch,
-            "layers": args.layers,
-            "dense_pages": int(plan["dense_indptr"][-1]),
-            "scored_pages_per_layer": nbytes["covered_pages"],
-            "max_chunk_size": batch.max_chunk,
-        },
-        "achieved_GBps": round(gbps, 1),
-        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "algorithmic_bytes_per_step": nbytes["step"],
-        "unfused_us_per_step": unfused,
-        "roofline": {
-            "kernel": f"{kernel} (CMean of the closed pages + q-mean + GeMV + top-k, one layer)",
-            "bound": "hbm",
-            "achieved": round(fused_gbps, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(fused_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(args.config),
-            "us_per_launch": round(us_fused, 3),
-            "bytes_per_launch": nbytes["fused"],
-        },
+        "config": {k: m[k] for k in ("workload", "batch", "layers", "dense_pages", "scored_pages_per_layer",
+                                     "max_chunk_size")},
+        "replay_us": st,
+        "achieved_GBps": m["achieved_GBps"],
+        "hbm_frac": round(m["achieved_GBps"] / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes_per_step": m["algorithmic_bytes_per_step"],
+        "unfused_us_per_step": m.get("unfused_us_per_step"),
+        "roofline": m["roofline"],
     }
-    if not args.no_cpu:
-        print("[bench] cpu baseline (oracle)", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(batch, step)
+    if "cpu_baseline" in m:
+        out["cpu_baseline"] = m["cpu_baseline"]
+    if args.config == "c2" and not args.no_extra:
+        # the other configurations of the scope table, measured the same way
+        extra = {}
+        for cfg in ("c3", "c5"):
+            m = measure_decode(cfg, args, dev)
+            extra[cfg] = {k: m[k] for k in ("workload", "us_per_step", "achieved_GBps", "roofline")}
+        b = bench_burst(args, dev)
+        extra["c4"] = {"workload": b["config"]["workload"], "us_per_burst": b["replay_us"],
+                       "achieved_GBps": b["achieved_GBps"], "separate_ops_us": b["separate_ops_us"],
+                       "roofline": b["roofline"]}
+        out["configs"] = extra
     return out
 
 
@@ -470,14 +534,21 @@ def bench_attention(args, dev) -> dict:
     }
 
 
-def traffic_probe(step: DecodeStep, dev) -> dict:
+def traffic_probe(step: DecodeStep, dev, unfused: bool = False) -> dict:
     """Kernels for a counter pass: every layer's fused indexer launch (twice:
     the second pass is the one to read, the first warms the code object and
-    the TLB like the timed replays), then a copy kernel of known size."""
+    the TLB like the timed replays), optionally the step with every op
+    launched on its own (GeMV, topK, CMean), then a copy kernel of known size."""
+    os.environ["VORTEX_FUSE"] = "1"
     step.run()  # the planner fills the block tables the kernels read
     with torch._C.DisableTorchFunctionSubclass():
         for _ in range(2):
             step.indexer_kernels_only()
+    if unfused:
+        os.environ["VORTEX_FUSE"] = "0"
+        step.run()
+        os.environ["VORTEX_FUSE"] = "1"
+    with torch._C.DisableTorchFunctionSubclass():
         n = 256 << 20  # bf16 elements: 512 MiB read + 512 MiB written
         src = torch.ones(n, dtype=torch.bfloat16, device=dev)
         dst = torch.empty_like(src)
@@ -525,8 +596,19 @@ def bench_burst(args, dev) -> dict:
     k_bytes = n_tiles * P * D * 2
     fused_bytes = k_bytes + 2 * n_tiles * D * 2 + loc.numel() * 8
     separate_bytes = 2 * (k_bytes + n_tiles * D * 2 + loc.numel() * 8)
-    us_fused = time_graph(capture(fused), args.steps, args.warmup) * 1000.0
-    us_sep = time_graph(capture(separate), max(5, args.steps // 2), 3) * 1000.0
+    if args.traffic_probe:
+        for _ in range(2):
+            fused()
+        separate()
+        n = 256 << 20  # bf16 elements: 512 MiB read + 512 MiB written
+        src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+        torch.neg(src, out=torch.empty_like(src))
+        torch.cuda.synchronize()
+        return {"probe": "traffic", "config": "c4", "copy_kernel": "neg (bf16)", "copy_read_bytes": 2 * n,
+                "copy_write_bytes": 2 * n}
+    st = replay_stats(time_replays(capture(fused), args.steps, args.warmup))
+    us_fused = st["median"]
+    us_sep = replay_stats(time_replays(capture(separate), max(10, args.steps // 2), 3))["median"]
     gbps = fused_bytes / (us_fused * 1e-6) / 1e9
     print(f"[bench] C4 fused {us_fused:.1f} us ({gbps:.0f} GB/s), separate {us_sep:.1f} us",
           file=sys.stderr, flush=True)
@@ -547,6 +629,7 @@ def bench_burst(args, dev) -> dict:
         "config": {"workload": "C4: page-finish burst, 65,536 pages x 8 heads (1,048,576 loc entries) "
                                "of a 70k-page pool, D 128, page 16, CMean + CMax bf16 outputs",
                    "pages": int(case.pages.numel()), "loc_entries": int(loc.numel())},
+        "replay_us": st,
         "achieved_GBps": round(gbps, 1),
         "separate_ops_us": round(us_sep, 2),
         "separate_ops_GBps": round(separate_bytes / (us_sep * 1e-6) / 1e9, 1),
@@ -557,7 +640,8 @@ def bench_burst(args, dev) -> dict:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get("c4"),
+            "us_per_launch": us_fused,
             "bytes_per_launch": fused_bytes,
         },
     }
