@@ -59,12 +59,14 @@ import workloads as W  # noqa: E402
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 HBM_PEAK_GBPS = 8000.0
 
-# HBM bytes per fused-indexer launch from the FETCH_SIZE and WRITE_SIZE
-# counter passes over --traffic-probe (each scaled by what the counter reads
-# for the probe's copy kernel of known size); the per-launch traffic does not
-# depend on the layer count (34,216 KiB read + 466 KiB written at C2, the
-# launch including the layer's CMean).
-TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_481_568}
+# HBM bytes per launch of each configuration's dominant kernel, from the
+# FETCH_SIZE and WRITE_SIZE counter passes over --traffic-probe (each scaled
+# by what the counter reads for the probe's copy kernel of known size: 0.5 for
+# FETCH_SIZE, 1.0 for WRITE_SIZE); the fused indexer launches include the
+# layer's decode CMean.  C2 17,111 KiB fetched + 466 KiB written per launch,
+# C3 17,107 + 464, C5 13,149 + 143, C4 (one pass of CMean + CMax over the
+# closed K tiles) 1,052,803 + 262,144.
+TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_515_625, "c3": 35_508_810, "c5": 27_074_227, "c4": 2_424_377_650}
 
 
 def _parse():
