@@ -279,7 +279,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   };
   bool active = is_active();
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
-  int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
+  int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
   int32_t* sel_pay = reinterpret_cast<int32_t*>(keys + a.row_cap);  // select_regs' payloads
 
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
     return;
   }
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
-  int32_t* sel_pay = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
+  int32_t* sel_pay = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(sel_pay + k);
   // the histograms of the final selection are cleared now, off its path (the
   // barriers of the arrival order this before the counting)
@@ -972,12 +972,12 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     const long long fill = eff_batch_size > 0 ? resident / eff_batch_size : 1;
     if (cps > fill) cps = fill;
     if (cps < 1) cps = 1;
-    const long long room = (kLdsBudget - (long long)a.topk * 12) / 2;
+    const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8 - (long long)a.topk * 4) / 2;
     long long cap = want < room ? want : room;
     cap &= ~7LL;
     if (cap < 0) cap = 0;
     a.row_cap = (int32_t)cap;
-    const size_t lds = (size_t)a.topk * 12 + (size_t)cap * 2;  // sel, its payloads, keys
+    const size_t lds = (size_t)vtx::sel_slots(a.topk) * 8 + (size_t)a.topk * 4 + (size_t)cap * 2;  // sel, payloads, keys
     long long items = (long long)eff_batch_size * cps + (a.x_out ? q_rows - eff_batch_size : 0);
     items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
     if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
@@ -987,12 +987,12 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
 
   // the planner's schedule, when it covers this launch's segments
   if (schedule && schedule_len >= vtx::sched_len(1, eff_batch_size)) a.sched = schedule;
-  const long long room = (kLdsBudget - (long long)a.topk * 12) / 6;
+  const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8 - (long long)a.topk * 4) / 6;
   long long cap = want < room ? want : room;
   cap &= ~7LL;
   if (cap < 0) cap = 0;
   a.row_cap = (int32_t)cap;
-  const size_t lds = (size_t)a.topk * 12 + (size_t)cap * 6;  // + select_regs' payloads
+  const size_t lds = (size_t)vtx::sel_slots(a.topk) * 8 + (size_t)a.topk * 4 + (size_t)cap * 6;  // + select_regs' payloads
   // With a q_mean output every query row gets a workgroup (rows past the
   // segments only write their mean).
   const long long grid = a.x_out ? q_rows : eff_batch_size;

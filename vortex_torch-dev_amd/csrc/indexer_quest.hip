@@ -96,7 +96,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   }
   const bool cached = n <= a.row_cap;
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
-  int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)k * sizeof(uint64_t));
+  int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
   const int32_t* dseg = a.didx + start;
   const uint16_t* qs = a.q + (long long)seg * G * D;
@@ -361,12 +361,12 @@ int quest_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   a.bos = reserved_bos;
   a.eos = reserved_eos;
   const long long want = max_num_pages > 0 ? max_num_pages : 0;
-  const long long room = (kLdsBudget - (long long)a.topk * 8) / 6;  // page id + key per page
+  const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8) / 6;  // page id + key per page
   long long cap = want < room ? want : room;
   cap &= ~7LL;
   if (cap < 0) cap = 0;
   a.row_cap = (int32_t)cap;
-  const size_t lds = (size_t)a.topk * 8 + (size_t)cap * 6;
+  const size_t lds = (size_t)vtx::sel_slots(a.topk) * 8 + (size_t)cap * 6;
   hipStream_t s = vtx::as_stream(stream);
   vtx::CmArgs cma{};
   const bool cm_launch = cm_inside && cms->nnz > 0;

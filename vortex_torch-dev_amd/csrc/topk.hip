@@ -49,7 +49,7 @@ __global__ __launch_bounds__(T) void topk_select_kernel(TopkArgs a) {
   if (obase < 0 || obase + k > a.sidx_len) return;
 
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
-  uint16_t* keys = reinterpret_cast<uint16_t*>(smem + (size_t)k * sizeof(uint64_t));
+  uint16_t* keys = reinterpret_cast<uint16_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   const uint16_t* sc = a.score + start;
 
   if (n <= a.key_cap) {
@@ -111,12 +111,12 @@ extern "C" int vtx_topk_select(const uint16_t* score, int64_t score_len,
   a.eos = reserved_eos;
 
   long long want = max_num_pages > 0 ? max_num_pages : 0;
-  const long long room = (kLdsBudget - (long long)topk_val * 8) / 2;
+  const long long room = (kLdsBudget - (long long)vtx::sel_slots(topk_val) * 8) / 2;
   long long cap = want < room ? want : room;
   cap &= ~7LL;
   if (cap < 0) cap = 0;
   a.key_cap = (int32_t)cap;
-  const size_t lds = (size_t)topk_val * 8 + (size_t)cap * 2;
+  const size_t lds = (size_t)vtx::sel_slots(topk_val) * 8 + (size_t)cap * 2;
 
   hipStream_t s = vtx::as_stream(stream);
   if (max_num_pages <= 512) {

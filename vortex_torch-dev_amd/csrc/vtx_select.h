@@ -72,6 +72,11 @@ __device__ __forceinline__ void sel_append(bool win, uint64_t comp, uint64_t* se
   }
 }
 
+// Winner slots allocated for a top-k of k: k rounded up to 16, the slots past
+// k held at zero, so a rank is counted over whole 16-slot blocks (a zero
+// slot never beats a winner: a composite is at least 1).
+__host__ __device__ constexpr int sel_slots(int k) { return (k + 15) & ~15; }
+
 __device__ __forceinline__ uint64_t sel_composite(uint32_t key, long long pos) {
   return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)pos);
 }
@@ -144,7 +149,7 @@ __device__ __forceinline__ void select_init(uint64_t* sel, int k, SelectShared<T
     sh.hist[1][i] = 0u;
   }
   if (tid == 0) sh.count = 0;
-  for (int j = tid; j < k; j += T) sel[j] = 0;  // decodes to a position >= n
+  for (int j = tid; j < sel_slots(k); j += T) sel[j] = 0;  // decodes to a position >= n
 }
 
 // Adds one item to the high-byte histogram (callers that produce the keys
@@ -285,26 +290,13 @@ __device__ __forceinline__ void select_topk(KeyAt key_at, long long n, int k, ui
   select_topk_counted<T>(key_at, n, k, sel, sh);
 }
 
-// Output rank of winner `c` among the k winners in sel (best = 0): eight
-// 8-byte LDS reads in flight (every lane reads the same composite, a
-// broadcast; 16-byte broadcast reads measured slower on gfx950).
-__device__ __forceinline__ int rank_of(uint64_t c, const uint64_t* sel, int k) {
-  int r = 0;
-  int m = 0;
-  for (; m + 8 <= k; m += 8) {
-#pragma unroll
-    for (int u = 0; u < 8; ++u) r += (sel[m + u] > c) ? 1 : 0;
-  }
-  for (; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
-  return r;
-}
-
-// Output rank of winner `c` among the k winners in sel, reading two
-// composites per 16-byte broadcast read (sel 16-byte aligned).
+// Output rank of winner `c` among the k winners in sel (best = 0): the
+// sel_slots(k) slots read two composites per 16-byte broadcast read, eight
+// reads in flight (sel 16-byte aligned, slots past k zero).
 __device__ __forceinline__ int rank_of_pairs(uint64_t c, const uint64_t* sel, int k) {
   int r = 0;
-  int m = 0;
-  for (; m + 16 <= k; m += 16) {
+  const int slots = sel_slots(k);
+  for (int m = 0; m < slots; m += 16) {
     U4 v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) v[u] = ld16(sel + m + 2 * u);
@@ -314,9 +306,10 @@ __device__ __forceinline__ int rank_of_pairs(uint64_t c, const uint64_t* sel, in
       r += (((uint64_t)v[u].w << 32 | v[u].z) > c) ? 1 : 0;
     }
   }
-  for (; m < k; ++m) r += (sel[m] > c) ? 1 : 0;
   return r;
 }
+
+__device__ __forceinline__ int rank_of(uint64_t c, const uint64_t* sel, int k) { return rank_of_pairs(c, sel, k); }
 
 // Position rank inside a wave of the scoring layout in which lane
 // l = grp * LPR + col holds pass position col * (64 / LPR) + grp: the number
