@@ -117,9 +117,11 @@ def fused_kernel_name(batch: W.DecodeBatch) -> str:
     if layout == 2 or (layout == 0 and segments < 2 * cus):
         small_pass = 32 if batch.head_dim <= 128 else 16
         mid = max(1, batch.max_pages_per_request - batch.bos - batch.eos)
-        large = segments * -(-mid // (4 * small_pass)) > 4 * cus
+        waves = 8 if batch.head_dim <= 256 else 4
+        large = segments * -(-mid // (waves * small_pass)) > (16 // waves) * cus
         cm = 4 if batch.batch <= 256 else 0  # the decode CMean in the launch (loc in four registers per lane)
-        return f"indexer_split_kernel<256, {lpr}, {vpl}, {small_pass * (2 if large else 1)}, {cm}>"
+        T = 512 if batch.head_dim <= 256 else 256
+        return f"indexer_split_kernel<{T}, {lpr}, {vpl}, {small_pass * (2 if large else 1)}, {cm}>"
     mp = batch.max_pages_per_request
     T = 256 if mp <= 256 else (512 if mp <= 1024 else 1024)
     # the decode CMean (loc: one token per request) runs in the same launch

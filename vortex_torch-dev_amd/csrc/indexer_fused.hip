@@ -761,23 +761,27 @@ int launch_dim(const FusedArgs& a, const vtx::CmArgs* cm, int blocks, size_t lds
   return vtx::check_launch("indexer_fused");
 }
 
-constexpr int kSplitThreads = 256;
+// Threads per split workgroup: 512 for rows of up to two vectors per lane
+// (the selecting workgroup then holds at most four of a 2046-page segment's
+// scores per thread: C3 17.2 us per launch against 20.9 us with 256 threads
+// and 18.3 with 1024), 256 for wider rows (two workgroups per CU fit their
+// registers; 512 threads measured 0.5 us slower at C5).
+int split_threads(int dim) { return dim <= 256 ? 512 : 256; }
 
 // Pages per wave pass of the split layout (small chunks; large ones are
 // twice this) and pages per split workgroup.
 int split_pass(int dim) { return dim <= 128 ? 32 : 16; }
-int split_chunk(int dim, bool large) { return (kSplitThreads / 64) * split_pass(dim) * (large ? 2 : 1); }
+int split_chunk(int dim, bool large) { return (split_threads(dim) / 64) * split_pass(dim) * (large ? 2 : 1); }
 
 template <int P, int kCm>
 int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
                     const vtx::CmArgs& cm) {
-  constexpr int T = kSplitThreads;
   switch (a.dim) {
-    case 64: indexer_split_kernel<T, 8, 1, 2 * P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
-    case 128: indexer_split_kernel<T, 16, 1, 2 * P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
-    case 256: indexer_split_kernel<T, 16, 2, P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
-    case 512: indexer_split_kernel<T, 16, 4, P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
-    case 576: indexer_split_kernel<T, 8, 9, P, kCm><<<blocks, T, lds, s>>>(a, counters, cps, cm); break;
+    case 64: indexer_split_kernel<512, 8, 1, 2 * P, kCm><<<blocks, 512, lds, s>>>(a, counters, cps, cm); break;
+    case 128: indexer_split_kernel<512, 16, 1, 2 * P, kCm><<<blocks, 512, lds, s>>>(a, counters, cps, cm); break;
+    case 256: indexer_split_kernel<512, 16, 2, P, kCm><<<blocks, 512, lds, s>>>(a, counters, cps, cm); break;
+    case 512: indexer_split_kernel<256, 16, 4, P, kCm><<<blocks, 256, lds, s>>>(a, counters, cps, cm); break;
+    case 576: indexer_split_kernel<256, 8, 9, P, kCm><<<blocks, 256, lds, s>>>(a, counters, cps, cm); break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch(kCm ? "indexer_fused (split, with CMean)" : "indexer_fused (split)");
@@ -961,10 +965,10 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   }
   if (split) {
     // Small chunks when every segment's chunks fit on the chip at once
-    // (four split workgroups per CU), else twice as large; past that,
+    // (16 waves of split workgroups per CU), else twice as large; past that,
     // workgroups loop over several chunks.
     const long long mid = want - reserved_bos - reserved_eos > 1 ? want - reserved_bos - reserved_eos : 1;
-    const long long resident = 4LL * cus;
+    const long long resident = (1024LL / split_threads(head_dim)) * cus;  // split workgroups resident at once
     const long long small = split_chunk(head_dim, false);
     const bool large = (long long)eff_batch_size * ((mid + small - 1) / small) > resident;
     const int chunk = split_chunk(head_dim, large);
