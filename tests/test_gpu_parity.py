@@ -296,6 +296,54 @@ def test_reduce_negative_and_out_of_range_loc(gpu):
     reduce_case(gpu, 50, 2, 16, 128, loc, O.MAX)
 
 
+def _f32_bits_to_bf16(a):
+    """fp32 array -> bf16 bits, round to nearest even (no NaNs here)."""
+    u = a.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("C", [64, 128, 256, 512])
+@pytest.mark.parametrize("R", [1, 3, 16, 24])
+def test_reduce_row_group_order_bits(gpu, C, R):
+    """The dim-1 CMean's fp32 summation order, bit for bit, for both tile
+    layouts of the page-reduce kernel (one lane per column vector for tiles of
+    up to 16 rows, row groups folded by a shuffle tree above that): rows are
+    split into G = 512 / C groups (group g: rows g, g + G, ... in order, from
+    0.0), the groups folded pairwise ((0 + 1) + (2 + 3)) + ..., divided by R
+    and rounded to bf16.  The in-launch decode CMean of the fused indexer uses
+    the same order (test_gpu_flow compares it with this launch bit for bit)."""
+    dev = gpu
+    H, n_pool, n_pages = 2, 40, 25
+    loc = torch.as_tensor(_burst_loc(n_pool, n_pages, R, 7), device=dev)
+    x = W.randn_bf16((n_pool * H, R, C), 11, dev)
+    out = torch.full((n_pool * H, 1, C), 7.0, device=dev, dtype=torch.bfloat16)
+    out2 = torch.full((n_pool * H, 1, C), 7.0, device=dev, dtype=torch.bfloat16)
+    _hip.page_reduce(x, out, loc, H, R, 1, _hip.REDUCE_MEAN)
+    _hip.page_reduce_multi(x, [out2], [O.MEAN], loc, H, R, 1)
+    torch.cuda.synchronize()
+    xf = _np(x.float()).astype(np.float32)  # [rows, R, C]
+    G = 512 // C
+
+    def fold(lo, hi):
+        if hi - lo == 1:
+            acc = np.zeros((xf.shape[0], C), np.float32)
+            for r in range(lo, R, G):
+                acc = (acc + xf[:, r, :]).astype(np.float32)
+            return acc
+        mid = (lo + hi) // 2
+        return (fold(lo, mid) + fold(mid, hi)).astype(np.float32)
+
+    mean = (fold(0, G) / np.float32(R)).astype(np.float32)
+    expect = _f32_bits_to_bf16(mean)
+    closed = sorted({int(v) // R for v in _np(loc) if (int(v) + 1) % R == 0})
+    rows = np.array([p * H + h for p in closed for h in range(H)])
+    got = _bits(out)[:, 0, :]
+    np.testing.assert_array_equal(got[rows], expect[rows])
+    np.testing.assert_array_equal(_bits(out2)[:, 0, :][rows], expect[rows])
+    untouched = np.setdiff1d(np.arange(n_pool * H), rows)
+    assert (got[untouched] == _bits(torch.tensor(7.0, dtype=torch.bfloat16))).all()
+
+
 def test_reduce_c4_burst_full_size(gpu):
     """C4 at full size: 65,536 pages (1,048,576 loc entries) of a 70k-page pool,
     CMean + CMax in one pass.  CMax must equal torch.amax of the same tiles

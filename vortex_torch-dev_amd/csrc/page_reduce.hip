@@ -12,9 +12,11 @@
 //     15 of 16 tokens that close nothing (the reference launches one program
 //     per (token, head) and returns early from most of them);
 //   * each wave then reduces whole (page, head) tiles: for dim 1 a row of C
-//     bf16 is split over C/8 lanes with one 16-byte load each, the remaining
-//     lanes take further rows, every lane accumulates fp32 over its rows and
-//     a shuffle tree folds the row groups together;
+//     bf16 is split over C/8 lanes with one 16-byte load each; with tiles of
+//     up to 16 rows each lane walks every row of its column (64/(C/8) tiles
+//     per wave at once, all rows in flight), otherwise the remaining lanes
+//     take further rows, every lane accumulates fp32 over its rows and a
+//     shuffle tree folds the row groups together (the same bits either way);
 //   * widths whose 16-byte column count does not divide 64 (D = 576) give
 //     each lane one column vector and load 8 rows of it at a time;
 //   * one pass over the tile feeds up to four outputs (the fused entry point),
@@ -54,7 +56,13 @@ __device__ __forceinline__ int collect_pages(const ReduceArgs& a, long long* fir
   return vtx::collect_pages<kThreads>(a, (long long)blockIdx.x * kThreads, first_row, wave_count);
 }
 
-// dim 1, C = 8 * LPR with LPR | 64: lane = (row group, 16-byte column vector).
+// dim 1, C = 8 * LPR with LPR | 64.  Bursts of tiles of up to 16 rows (and
+// a statistic set whose registers fit): lane = (tile slot, 16-byte column
+// vector), a wave takes 64 / LPR tiles at once and each lane reduces all rows
+// of its column alone (vtx::tile_stats_lane), so all of a tile's rows are in
+// flight together, nothing crosses lanes and every lane writes its own
+// outputs.  Otherwise lane = (row group, column vector), one tile per wave,
+// folded by an xor tree (vtx::tile_stats_vec).  Both give the same bits.
 // NEED: statistics to accumulate (kNeed* mask covering every output's type).
 template <int LPR, int NEED>
 __global__ __launch_bounds__(kThreads) void reduce_rows_vec_kernel(ReduceArgs a) {
@@ -68,6 +76,24 @@ __global__ __launch_bounds__(kThreads) void reduce_rows_vec_kernel(ReduceArgs a)
   const int R = a.rows_per_tile;
   const int tiles = pages * a.heads;
 
+  if constexpr (vtx::lane_tiles_fit<LPR, NEED>()) {
+    // (a decode-sized loc, whose few tiles are spread over several
+    // workgroups, keeps one tile per wave: more waves share the latency)
+    if (R <= 16 && gridDim.y == 1) {  // uniform
+      constexpr int kSlots = vtx::kWave / LPR;  // tiles per wave at once; lane group grp takes slot grp
+      for (int t0 = (blockIdx.y * kWavesPerBlock + wave) * kSlots; t0 < tiles;
+           t0 += gridDim.y * kWavesPerBlock * kSlots) {
+        const int t = t0 + grp;
+        if (t >= tiles) continue;
+        const long long row = first_row[t / a.heads] + (t % a.heads);
+        if (!vtx::tile_in_range(a, row)) continue;
+        Acc acc[8];
+        vtx::tile_stats_lane<LPR, NEED>(a.x, row, R, a.cols, cv, acc);
+        vtx::tile_store_vec(a, row, cv, acc);
+      }
+      return;
+    }
+  }
   for (int t = blockIdx.y * kWavesPerBlock + wave; t < tiles; t += gridDim.y * kWavesPerBlock) {
     const long long row = first_row[t / a.heads] + (t % a.heads);
     if (!vtx::tile_in_range(a, row)) continue;
