@@ -99,12 +99,13 @@ __device__ __forceinline__ void query_mean_lds(const FusedArgs& a, const uint16_
       }
 #pragma unroll
       for (int j = 0; j < kRowsIn; ++j) {
-        if (g0 + j < a.G) {
-          float f[8];
-          vtx::unpack8(r[j], f);
+        // a select, not a branch (a branch lets the compiler sink the load
+        // into it and wait for each row on its own)
+        const bool in = g0 + j < a.G;
+        float f[8];
+        vtx::unpack8(r[j], f);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[j % 4][e] += f[e];
-        }
+        for (int e = 0; e < 8; ++e) acc[j % 4][e] = in ? acc[j % 4][e] + f[e] : acc[j % 4][e];
       }
     }
     uint32_t b[8];
@@ -230,14 +231,17 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   int tile_rank = blockIdx.x;  // this workgroup's share of the CMean tiles
   int32_t pe[3] = {0, 0, 0};   // predicted dense begin, dense end, sparse begin
   if (a.sched) {               // uniform
+    // header and entry loaded together, before any is looked at (one round
+    // trip); workgroups past the segments read the last entry and ignore it
+    const bool mine = (int)blockIdx.x < a.segments;
+    const int32_t* e = a.sched + 4 + 4 * (long long)(mine ? blockIdx.x : a.segments - 1);
     const int32_t h0 = a.sched[0], h1 = a.sched[1], h2 = a.sched[2];
-    const bool ok = h0 == vtx::kSchedMagic && h1 == a.segments && h2 >= 1;
-    if ((int)blockIdx.x < a.segments) {
-      const int32_t* e = a.sched + 4 + 4 * (long long)blockIdx.x;
-      const int32_t e0 = e[0];
-      pe[0] = e[1];
-      pe[1] = e[2];
-      pe[2] = e[3];
+    const int32_t e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3];
+    const bool ok = (h0 == vtx::kSchedMagic) & (h1 == a.segments) & (h2 >= 1);
+    if (mine) {
+      pe[0] = e1;
+      pe[1] = e2;
+      pe[2] = e3;
       if (ok && e0 >= 0 && e0 < a.segments) {
         seg = e0;
         predicted = true;
@@ -264,11 +268,13 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   const int q_rows_in = a.G > 0 ? a.G : 1;
   const uint16_t* qb = a.G > 0 ? a.q + (long long)seg * a.G * D : a.x + (long long)seg * D;
   if (q_in_regs) {
+    // rows past G load row G - 1 again (query_row reads only the first G):
+    // no branch around a load, so nothing waits for them here
 #pragma unroll
     for (int g = 0; g < kQRegs; ++g)
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
-        qv[g][v] = g < q_rows_in ? vtx::ld16(qb + (long long)g * D + (v * LPR + col) * 8) : vtx::U4{0u, 0u, 0u, 0u};
+        qv[g][v] = vtx::ld16(qb + (long long)(g < q_rows_in ? g : q_rows_in - 1) * D + (v * LPR + col) * 8);
   }
 
   vtx::Closing<kLocRegs> closing{};
@@ -528,10 +534,14 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   const long long chunk_items = (long long)a.segments * cps;
   vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
-  if constexpr (cm_on) {
-    closing = vtx::closing_build(cma, cm_pos);
-    n_close = closing.count;
-  }
+  // the closed pages of loc (waits for the loc loads: called once the
+  // work id's other first loads are issued)
+  auto build_closing = [&]() {
+    if constexpr (cm_on) {
+      closing = vtx::closing_build(cma, cm_pos);
+      n_close = closing.count;
+    }
+  };
   // this work id's share of the CMean tiles (after its scores are counted in)
   auto cm_tiles = [&]() {
     if constexpr (cm_on) {
@@ -543,6 +553,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   float xs[VPL][8];
   vtx::U4 qv[kQRegs][VPL];
   if (w >= chunk_items) {  // query rows past the segments: only their mean
+    build_closing();
     const long long row = a.segments + (w - chunk_items);
     if (a.x_out && a.G > 0 && row < a.q_rows) {
       if (a.G <= kQRegs)
@@ -557,19 +568,25 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   const int c = (int)(w % cps);
   const bool store_mean = c == 0 && wave == 0 && grp == 0;
 
+  // the segment's bounds in one vector load (lane 0: dense begin, lane 1:
+  // dense end, lane 2: sparse begin; one round trip, where three scalar-path
+  // loads would each wait for the one before)
+  const int32_t* bp = lane == 1 ? a.dindptr + seg + 1 : lane == 2 ? a.sindptr + seg : a.dindptr + seg;
+  const int32_t bv = *bp;
   const bool q_in_regs = a.G > 0 && a.G <= kQRegs;
   const uint16_t* qb = a.G > 0 ? a.q + (long long)seg * a.G * D : a.x + (long long)seg * D;
-  if (q_in_regs) {
+  if (q_in_regs) {  // rows past G load row G - 1 again (query_row reads only the first G)
 #pragma unroll
     for (int g = 0; g < kQRegs; ++g)
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
-        qv[g][v] = g < a.G ? vtx::ld16(qb + (long long)g * D + (v * LPR + col) * 8) : vtx::U4{0u, 0u, 0u, 0u};
+        qv[g][v] = vtx::ld16(qb + (long long)(g < a.G ? g : a.G - 1) * D + (v * LPR + col) * 8);
   }
+  build_closing();
 
-  const long long start = (long long)a.dindptr[seg] + a.bos;
-  const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
-  const long long obase = (long long)a.sindptr[seg] + a.bos;
+  const long long start = (long long)__builtin_amdgcn_readlane(bv, 0) + a.bos;
+  const long long n = (long long)__builtin_amdgcn_readlane(bv, 1) - a.eos - start;
+  const long long obase = (long long)__builtin_amdgcn_readlane(bv, 2) + a.bos;
   bool active = k > 0 && n > k;
   if (active && (start < 0 || start + n > a.score_len || start + n > a.didx_len || obase < 0 ||
                  obase + k > a.sidx_len))
