@@ -109,16 +109,17 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     int r = -1;
     for (int g0 = 0; g0 < G; g0 += kG) {
       float xs[kG][VPL][8];
+      // heads past G read head G - 1 and are zeroed by a select (no branch
+      // around the load, which would make the wave wait for it there)
 #pragma unroll
       for (int gg = 0; gg < kG; ++gg)
 #pragma unroll
         for (int v = 0; v < VPL; ++v) {
-          if (g0 + gg < G) {
-            vtx::unpack8(vtx::ld16(qs + (long long)(g0 + gg) * D + (v * LPR + col) * 8), xs[gg][v]);
-          } else {
+          const bool in = g0 + gg < G;
+          float f[8];
+          vtx::unpack8(vtx::ld16(qs + (long long)(in ? g0 + gg : G - 1) * D + (v * LPR + col) * 8), f);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) xs[gg][v][e] = 0.f;
-          }
+          for (int e = 0; e < 8; ++e) xs[gg][v][e] = in ? f[e] : 0.f;
         }
       float sc[kG];
       vtx::score_pass_multi<LPR, VPL, kPass, kG>(a.y, a.y_rows, D, my_row, cnt, xs, grp, col, &r, sc);
@@ -168,31 +169,36 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   }
   __syncthreads();
 
-  // ---- softmax statistics of each query head over the segment
-  auto raw_at = [&](long long i, int g) -> float {
-    return vtx::bf16_to_f32(cached ? raw[i * G + g] : sc_out[i * G + g]);
-  };
-  if (a.softmax) {
-    float vals[vtx::kScanRegs];
-    bool in_regs;
-    vtx::column_scan_stats(raw_at, n, G, a.scale, true, pm, ps, vals, in_regs);
-  }
-
-  // ---- softmax values, maximum over the query heads, keys
-  for (long long i = tid; i < n; i += T) {
-    float m = -INFINITY;
-    for (int g = 0; g < G; ++g) {
-      const float v = raw_at(i, g);
-      const uint32_t o = a.softmax ? vtx::f32_to_bf16(vtx::softmax_value(v, a.scale, pm[g], ps[g]))
-                                   : vtx::f32_to_bf16(v);
-      sc_out[i * G + g] = (uint16_t)o;
-      m = fmaxf(m, vtx::bf16_to_f32(o));
+  // ---- softmax statistics of each query head over the segment, then the
+  // softmax values, their maximum over the query heads and the keys.  The
+  // raw scores are read through a pointer of one kind per path (LDS when
+  // cached, global otherwise), so the reads are LDS reads, not generic ones.
+  auto stats_and_keys = [&](auto raw_at) {
+    if (a.softmax) {
+      float vals[vtx::kScanRegs];
+      bool in_regs;
+      vtx::column_scan_stats(raw_at, n, G, a.scale, true, pm, ps, vals, in_regs);
     }
-    const uint32_t ab = vtx::f32_to_bf16(m);
-    a.aggr[start + i] = (uint16_t)ab;
-    const uint32_t key = vtx::score_key(ab);
-    if (cached) keys[i] = (uint16_t)key;
-    vtx::select_count<T>(key, sh);
+    for (long long i = tid; i < n; i += T) {
+      float m = -INFINITY;
+      for (int g = 0; g < G; ++g) {
+        const float v = raw_at(i, g);
+        const uint32_t o = a.softmax ? vtx::f32_to_bf16(vtx::softmax_value(v, a.scale, pm[g], ps[g]))
+                                     : vtx::f32_to_bf16(v);
+        sc_out[i * G + g] = (uint16_t)o;
+        m = fmaxf(m, vtx::bf16_to_f32(o));
+      }
+      const uint32_t ab = vtx::f32_to_bf16(m);
+      a.aggr[start + i] = (uint16_t)ab;
+      const uint32_t key = vtx::score_key(ab);
+      if (cached) keys[i] = (uint16_t)key;
+      vtx::select_count<T>(key, sh);
+    }
+  };
+  if (cached) {  // uniform
+    stats_and_keys([&](long long i, int g) -> float { return vtx::bf16_to_f32(raw[i * G + g]); });
+  } else {
+    stats_and_keys([&](long long i, int g) -> float { return vtx::bf16_to_f32(sc_out[i * G + g]); });
   }
   __syncthreads();
 

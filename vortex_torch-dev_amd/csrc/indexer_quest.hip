@@ -121,16 +121,17 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
     float best = -INFINITY;
     for (int g0 = 0; g0 < G; g0 += kG) {
       float xs[kG][VPL][8];
+      // heads past G read head G - 1 and are zeroed by a select (no branch
+      // around the load, which would make the wave wait for it there)
 #pragma unroll
       for (int gg = 0; gg < kG; ++gg)
 #pragma unroll
         for (int v = 0; v < VPL; ++v) {
-          if (g0 + gg < G) {
-            vtx::unpack8(vtx::ld16(qs + (long long)(g0 + gg) * D + (v * LPR + col) * 8), xs[gg][v]);
-          } else {
+          const bool in = g0 + gg < G;
+          float f[8];
+          vtx::unpack8(vtx::ld16(qs + (long long)(in ? g0 + gg : G - 1) * D + (v * LPR + col) * 8), f);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) xs[gg][v][e] = 0.f;
-          }
+          for (int e = 0; e < 8; ++e) xs[gg][v][e] = in ? f[e] : 0.f;
         }
       float sc[kG];
       vtx::quest_pass_multi<LPR, VPL, kPass, kG>(a.ymax, a.ymin, a.y_rows, D, my_row, cnt, xs, grp, col, &r, sc);

@@ -31,12 +31,20 @@ __device__ __forceinline__ void column_scan_stats(ValAt val_at, long long cnt, i
   const int r0 = tid / cols;
   const bool active = tid < kScanThreads && r0 < per_col;
   in_regs = cnt <= (long long)per_col * kScanRegs;  // uniform
-  if (in_regs) {
+  if (in_regs && cnt > 0) {
+    // every read issued before any is used: rows past cnt (and threads past
+    // the scan) read row 0 and drop it through a select, with no branch
+    // around a read for the compiler to sink it into
 #pragma unroll
     for (int k = 0; k < kScanRegs; ++k) {
       const long long r = r0 + (long long)k * per_col;
-      vals[k] = (active && r < cnt) ? val_at(r, c) : 0.f;
+      const bool in = active && r < cnt;
+      const float v = val_at(in ? r : 0, c);
+      vals[k] = in ? v : 0.f;
     }
+  } else if (in_regs) {
+#pragma unroll
+    for (int k = 0; k < kScanRegs; ++k) vals[k] = 0.f;
   }
   float m = -1e30f, s = 0.f;
   auto add = [&](float v) {
