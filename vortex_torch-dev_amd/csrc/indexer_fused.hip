@@ -719,16 +719,14 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const long long i = base + (long long)u * T + tid;
-      v[u] = i < n ? load_coherent(scs + i) : (uint16_t)0;
+      v[u] = load_coherent(scs + (i < n ? i : n - 1));  // past n: position n - 1, not used
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const long long i = base + (long long)u * T + tid;
-      if (i < n) {
-        const uint32_t key = vtx::score_key(v[u]);
-        if (cached) keys[i] = (uint16_t)key;
-        vtx::select_count<T>(key, sh);
-      }
+      const uint32_t key = vtx::score_key(v[u]);
+      if (cached) keys[i < n ? i : n - 1] = (uint16_t)key;  // past n: position n - 1's own key again
+      if (i < n) vtx::select_count<T>(key, sh);
     }
   }
   __syncthreads();

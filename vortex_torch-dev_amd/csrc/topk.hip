@@ -55,16 +55,18 @@ __global__ __launch_bounds__(T) void topk_select_kernel(TopkArgs a) {
   if (n <= a.key_cap) {
     constexpr int kU = 4;  // score loads in flight per thread
     for (long long i0 = 0; i0 < n; i0 += (long long)T * kU) {
+      // positions past n read (and rewrite) position n - 1: no branch around
+      // a load, which would let the compiler wait for each load on its own
       uint16_t v[kU];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const long long i = i0 + (long long)u * T + tid;
-        v[u] = i < n ? sc[i] : (uint16_t)0;
+        v[u] = sc[i < n ? i : n - 1];
       }
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const long long i = i0 + (long long)u * T + tid;
-        if (i < n) keys[i] = (uint16_t)vtx::score_key(v[u]);
+        keys[i < n ? i : n - 1] = (uint16_t)vtx::score_key(v[u]);
       }
     }
     __syncthreads();

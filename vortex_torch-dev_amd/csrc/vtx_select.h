@@ -174,13 +174,15 @@ __device__ __forceinline__ void select_topk_counted(KeyAt key_at, long long n, i
   sel_find_bin(sh, 0, (uint32_t)k, &hi_bin, &above_hi);
   const uint32_t hi = (uint32_t)hi_bin;
 
-  // kSelU keys per thread per round, their reads issued together; the keys
+  // kSelU keys per thread per round, their reads issued together (positions
+  // past n read position n - 1, ignored by every use: no branch around a
+  // read, which would let the compiler wait for each on its own); the keys
   // of the first round stay in registers for the second pass.
   auto load = [&](long long i0, uint32_t (&key)[kSelU]) {
 #pragma unroll
     for (int u = 0; u < kSelU; ++u) {
       const long long i = i0 + (long long)u * T + tid;
-      key[u] = i < n ? key_at(i) : 0u;
+      key[u] = key_at(i < n ? i : n - 1);
     }
   };
   auto count_lo = [&](long long i0, const uint32_t (&key)[kSelU]) {
