@@ -84,6 +84,17 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
     const long long t = (m - 1) * P + last;
     T_tok = t < (1LL << 30) ? (int)t : 0;  // (token indices, with the prefetch past the end, fit an int)
   }
+  // query slice of this lane (columns (v * LPR + col) * 8 .. + 8), requested
+  // first so that it arrives with the page rows; heads past G read head
+  // G - 1 and are zeroed by a select (no branch around the load, which would
+  // make the wave wait for it there)
+  vtx::U4 qraw[kG][VPL];
+#pragma unroll
+  for (int g = 0; g < kG; ++g)
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+      qraw[g][v] = vtx::ld16(a.q + ((long long)seg * G + (g < G ? g : G - 1)) * D + (v * LPR + col) * 8);
+
   // the segment's page rows (-1: outside the pool)
   const bool staged = m <= kPageCap;
   if (staged && T_tok > 0) {
@@ -93,18 +104,15 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
     }
   }
 
-  // query slice of this lane (columns (v * LPR + col) * 8 .. + 8)
   float qs[kG][VPL][8];
 #pragma unroll
   for (int g = 0; g < kG; ++g)
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
-      if (g < G) {
-        vtx::unpack8(vtx::ld16(a.q + ((long long)seg * G + g) * D + (v * LPR + col) * 8), qs[g][v]);
-      } else {
+      float f[8];
+      vtx::unpack8(qraw[g][v], f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qs[g][v][e] = 0.f;
-      }
+      for (int e = 0; e < 8; ++e) qs[g][v][e] = g < G ? f[e] : 0.f;
     }
 
   float mx[kG], l[kG], acc[kG][VPL][8];
