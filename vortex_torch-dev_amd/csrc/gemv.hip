@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kThreads, (VPL == 1 ? 4 : 2)) void gemv_paged_kerne
         for (int t = 0; t < half; ++t) {
           const float send = upper ? acc[t] : acc[t + half];
           const float keep = upper ? acc[t + half] : acc[t];
-          acc[t] = keep + __shfl_xor(send, half, vtx::kWave);
+          acc[t] = keep + vtx::xshfl(send, half);
         }
       }
       // This lane now owns slot `col`, i.e. row col * kRowsPerLoad + grp.

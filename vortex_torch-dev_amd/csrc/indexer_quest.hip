@@ -51,7 +51,7 @@ __device__ __forceinline__ float quest_vec(const vtx::U4& mx, const vtx::U4& mn,
 #pragma unroll
   for (int e = 0; e < 8; ++e) s += vtx::bf16r(fmaxf(xs[e] * a[e], xs[e] * b[e]));
 #pragma unroll
-  for (int d = LPR / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d, vtx::kWave);
+  for (int d = LPR / 2; d >= 1; d >>= 1) s += vtx::xshfl(s, d);
   return s;
 }
 

@@ -150,7 +150,7 @@ __device__ __forceinline__ float score_vec(const U4& cen, const float (&xs)[1][8
   const U4 row[1] = {cen};
   float f = dot_row<1>(row, xs);
 #pragma unroll
-  for (int d = LPR / 2; d >= 1; d >>= 1) f += __shfl_xor(f, d, kWave);
+  for (int d = LPR / 2; d >= 1; d >>= 1) f += xshfl(f, d);
   return f;
 }
 
@@ -256,7 +256,7 @@ template <int LPR, int VPL>
 __device__ __forceinline__ float score_vec_rows(const U4 (&cen)[VPL], const float (&xs)[VPL][8]) {
   float f = dot_row<VPL>(cen, xs);
 #pragma unroll
-  for (int d = LPR / 2; d >= 1; d >>= 1) f += __shfl_xor(f, d, kWave);
+  for (int d = LPR / 2; d >= 1; d >>= 1) f += xshfl(f, d);
   return f;
 }
 

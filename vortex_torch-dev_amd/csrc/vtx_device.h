@@ -65,10 +65,52 @@ __device__ __forceinline__ int uniform(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
+// v of lane (lane ^ d).  For d = 1, 2, 4, 8, 16 or 32 known at compile time
+// (after unrolling) this is VALU only: DPP row operations for d <= 8 (quad
+// permutes, the two 4-lane row shifts and a select, an 8-lane row rotate)
+// and gfx950's permlane swaps between 16-lane rows and 32-lane halves, about
+// a third of the dependent latency of the LDS permute behind __shfl_xor
+// (measured: 24 against 71 cycles per shuffle-and-add step); any other d
+// falls back to __shfl_xor.  Every lane of the wave must be active.
+__device__ __forceinline__ uint32_t xshfl_u32(uint32_t v, int d) {
+  if (__builtin_constant_p(d)) {
+    const int lane = lane_id();
+    switch (d) {
+      case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+      case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+      case 4: {
+        const int up = __builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0xF, false);  // row_shl:4 (lane + 4)
+        const int dn = __builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4 (lane - 4)
+        return (uint32_t)((lane & 4) ? dn : up);
+      }
+      case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+      case 16: {
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? p[0] : p[1];
+      }
+      case 32: {
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? p[0] : p[1];
+      }
+      default: break;
+    }
+  }
+  return (uint32_t)__shfl_xor((int)v, d, kWave);
+}
+__device__ __forceinline__ float xshfl(float v, int d) {
+  return __uint_as_float(xshfl_u32(__float_as_uint(v), d));
+}
+__device__ __forceinline__ uint32_t xshfl(uint32_t v, int d) { return xshfl_u32(v, d); }
+__device__ __forceinline__ int xshfl(int v, int d) { return (int)xshfl_u32((uint32_t)v, d); }
+__device__ __forceinline__ long long xshfl(long long v, int d) {
+  const uint64_t u = (uint64_t)v;
+  return (long long)(((uint64_t)xshfl_u32((uint32_t)(u >> 32), d) << 32) | xshfl_u32((uint32_t)u, d));
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  for (int d = 32; d >= 1; d >>= 1) v += xshfl(v, d);
   return v;
 }
 

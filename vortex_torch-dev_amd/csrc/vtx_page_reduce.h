@@ -65,10 +65,10 @@ __device__ __forceinline__ void acc_add_if(Acc& a, float v, bool in) {
 }
 template <int NEED = kNeedAll>
 __device__ __forceinline__ void acc_merge_xor(Acc& a, int d) {
-  if constexpr ((NEED & kNeedSum) != 0) a.sum += __shfl_xor(a.sum, d, kWave);
-  if constexpr ((NEED & kNeedSq) != 0) a.sq += __shfl_xor(a.sq, d, kWave);
-  if constexpr ((NEED & kNeedMax) != 0) a.mx = fmaxf(a.mx, __shfl_xor(a.mx, d, kWave));
-  if constexpr ((NEED & kNeedMin) != 0) a.mn = fminf(a.mn, __shfl_xor(a.mn, d, kWave));
+  if constexpr ((NEED & kNeedSum) != 0) a.sum += xshfl(a.sum, d);
+  if constexpr ((NEED & kNeedSq) != 0) a.sq += xshfl(a.sq, d);
+  if constexpr ((NEED & kNeedMax) != 0) a.mx = fmaxf(a.mx, xshfl(a.mx, d));
+  if constexpr ((NEED & kNeedMin) != 0) a.mn = fminf(a.mn, xshfl(a.mn, d));
 }
 // Final value of reduction `type` over `count` elements, rounded to bf16 bits.
 __device__ __forceinline__ uint32_t acc_value(const Acc& a, int type, int count) {

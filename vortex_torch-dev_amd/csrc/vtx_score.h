@@ -78,12 +78,12 @@ __device__ __forceinline__ void row_pass(const uint16_t* const (&ys)[kRows], lon
       for (int t = 0; t < half; ++t) {
         const float send = upper ? acc[g][t] : acc[g][t + half];
         const float keep = upper ? acc[g][t + half] : acc[g][t];
-        acc[g][t] = keep + __shfl_xor(send, stride, kWave);
+        acc[g][t] = keep + xshfl(send, stride);
       }
     }
     constexpr int kShare = LPR / kSlots;  // lanes holding the same slot
 #pragma unroll
-    for (int d = kShare / 2; d >= 1; d >>= 1) acc[g][0] += __shfl_xor(acc[g][0], d, kWave);
+    for (int d = kShare / 2; d >= 1; d >>= 1) acc[g][0] += xshfl(acc[g][0], d);
     sc[g] = acc[g][0];
   }
   constexpr int kShare = LPR / kSlots;
