@@ -203,6 +203,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   constexpr bool kRegSelect = VPL == 1 && (LPR == 8 || LPR == 16) && kPass / kRowsPerLoad == LPR;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
+  __shared__ vtx::BitonicShared<T> bsh;  // kRegSelect with k <= 32: the bitonic select
   __shared__ __align__(16) uint16_t qm_row[VPL * LPR * 8];  // query mean, G > kQRegs
 
   const int tid = threadIdx.x;
@@ -372,6 +373,9 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
 
   if constexpr (kRegSelect) {
     if (n <= (long long)kWaves * kPass) {  // uniform: at most one pass per wave
+      // k <= 32 with the row ids in LDS: the bitonic select; else the radix
+      // select on registers (select_regs)
+      const bool bitonic = k <= vtx::kMaxBitonicK && n <= a.row_cap;  // uniform
       bool have = false, deferred = false;
       uint32_t key = 0;
       int rid = -1, r = -1;
@@ -390,7 +394,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
             const uint32_t sb = vtx::f32_to_bf16(sc);
             key = vtx::score_key(sb);
             a.score[start + p0 + r] = (uint16_t)sb;
-            vtx::select_count<T>(key, sh);
+            if (!bitonic) vtx::select_count<T>(key, sh);
             have = true;
           }
         }
@@ -406,14 +410,21 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
             const uint32_t sb = vtx::f32_to_bf16(f);
             key = vtx::score_key(sb);
             a.score[start + p0 + r] = (uint16_t)sb;
-            vtx::select_count<T>(key, sh);
+            if (!bitonic) vtx::select_count<T>(key, sh);
             have = true;
           }
         }
       }
-      __syncthreads();  // every key counted
-      vtx::select_regs<T, LPR>(have, key, p0 + r, rid, k, sel, sel_pay, sh,
-                               [&](int rank, int payload) { a.sidx[obase + rank] = payload; });
+      if (bitonic) {
+        if (have) rows[p0 + r] = rid;  // payload by position (visible after the select's first barrier)
+        vtx::select_bitonic<T>(vtx::bitonic_comp(have, key, (int)(p0 + r)), k, bsh, [&](int rank, uint32_t c) {
+          a.sidx[obase + rank] = rows[vtx::bitonic_position(c)];
+        });
+      } else {
+        __syncthreads();  // every key counted
+        vtx::select_regs<T, LPR>(have, key, p0 + r, rid, k, sel, sel_pay, sh,
+                                 [&](int rank, int payload) { a.sidx[obase + rank] = payload; });
+      }
       cm_tiles();
       return;
     }

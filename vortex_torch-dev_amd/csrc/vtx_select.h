@@ -470,4 +470,78 @@ __device__ __forceinline__ void select_emit(const uint64_t* sel, int k, long lon
   }
 }
 
+// ---------------------------------------------------------------------------
+// Bitonic top-k for k <= 32 with at most one item per lane (the fused
+// indexer's one-pass segments).  An item is the 32-bit composite
+// (key << 16) | (0xffff - position) (positions below 65536; 0 = no item): a
+// larger composite is a larger key, then a lower position — the order of a
+// stable descending sort, and unique per item.  Each wave sorts its 64
+// composites with a bitonic network (21 compare-exchange steps on VALU
+// shuffles, no barrier, overlapping the other waves' loads), keeps its best
+// 32 in LDS, and the lists are merged pairwise (a 32-descending list against
+// a reversed one is bitonic: 6 steps) until wave 0 holds the best 32 in
+// order.  kMaxBitonicK is the largest k it serves.
+constexpr int kMaxBitonicK = 32;
+
+__device__ __forceinline__ uint32_t bitonic_comp(bool have, uint32_t key, int pos) {
+  return have ? ((key << 16) | (0xffffu - (uint32_t)pos)) : 0u;
+}
+__device__ __forceinline__ int bitonic_position(uint32_t comp) { return (int)(0xffffu - (comp & 0xffffu)); }
+
+// The wave's 64 values sorted descending (lane 0 the largest).  Every lane
+// of the wave must be active.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t v) {
+  const int i = lane_id();
+#pragma unroll
+  for (int k2 = 2; k2 <= kWave; k2 <<= 1)
+#pragma unroll
+    for (int j = k2 >> 1; j > 0; j >>= 1) {
+      const uint32_t o = xshfl_u32(v, j);
+      const bool keep_max = ((i & j) == 0) == ((i & k2) == 0);
+      v = keep_max ? (v > o ? v : o) : (v < o ? v : o);
+    }
+  return v;
+}
+
+// A bitonic sequence over the wave's 64 lanes sorted descending.
+__device__ __forceinline__ uint32_t wave_merge_desc(uint32_t v) {
+  const int i = lane_id();
+#pragma unroll
+  for (int j = kWave / 2; j > 0; j >>= 1) {
+    const uint32_t o = xshfl_u32(v, j);
+    v = (i & j) == 0 ? (v > o ? v : o) : (v < o ? v : o);
+  }
+  return v;
+}
+
+// LDS of select_bitonic: two buffers of 32 composites per wave.
+template <int T>
+struct BitonicShared {
+  uint32_t cand[2][(T / kWave) * 32];
+};
+
+// The k (<= 32) best composites of the workgroup, emit(rank, comp) for rank
+// 0 .. k-1 (called by lanes 0 .. k-1 of wave 0).  Every thread of the
+// workgroup calls it with its item (0: none); it contains barriers.
+template <int T, typename Emit>
+__device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShared<T>& bs, Emit emit) {
+  constexpr int kWaves = T / kWave;
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  uint32_t v = wave_sort_desc(comp);
+  if (lane < 32) bs.cand[0][wave * 32 + lane] = v;
+  int buf = 0;
+#pragma unroll
+  for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 32 become w / 2
+    __syncthreads();
+    if (wave < w / 2) {  // uniform
+      const int src = lane < 32 ? (2 * wave) * 32 + lane : (2 * wave + 1) * 32 + (kWave - 1 - lane);
+      v = wave_merge_desc(bs.cand[buf][src]);
+      if (w > 2 && lane < 32) bs.cand[buf ^ 1][wave * 32 + lane] = v;
+    }
+    buf ^= 1;
+  }
+  if (wave == 0 && lane < k) emit(lane, v);
+}
+
 }  // namespace vtx
