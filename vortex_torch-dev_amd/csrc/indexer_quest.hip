@@ -73,6 +73,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
+  __shared__ vtx::BitonicShared<T> bsh;  // cached segments of up to T pages with k <= 32
 
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
@@ -190,7 +191,15 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   }
   __syncthreads();
 
-  // ---- top-k of the segment
+  // ---- top-k of the segment: the bitonic select (one key per thread, from
+  // LDS) when every page fits one thread each and k <= 32, else the radix
+  // select over the counted keys
+  if (cached && n <= T && k <= vtx::kMaxBitonicK) {  // uniform
+    const int i = threadIdx.x;
+    const uint32_t comp = vtx::bitonic_comp(i < n, i < n ? (uint32_t)keys[i] : 0u, i);
+    vtx::select_bitonic<T>(comp, k, bsh, [&](int rk, uint32_t c) { a.sidx[obase + rk] = rows[vtx::bitonic_position(c)]; });
+    return;
+  }
   if (cached) {
     vtx::select_topk_counted<T>([&](long long i) { return (uint32_t)keys[i]; }, n, k, sel, sh);
   } else {
