@@ -6,7 +6,9 @@
 // best pages, best first, ties resolved toward the lower position.
 //
 // Instead of sorting the whole segment this kernel selects and then orders
-// only the k winners.  One workgroup per segment: every score becomes a
+// only the k winners.  One workgroup per segment.  A segment of at most one
+// page per thread with k <= 32 takes the bitonic select (vtx_select.h).
+// Otherwise every score becomes a
 // 16-bit order key (bf16 bits with the sign folded, -0.0 == +0.0), cached in
 // LDS; a two-pass radix select (vtx_select.h) collects the k winners; each
 // winner's output rank is the number of winners with a larger composite
@@ -35,6 +37,7 @@ template <int T>
 __global__ __launch_bounds__(T) void topk_select_kernel(TopkArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T> sh;
+  __shared__ vtx::BitonicShared<T> bsh;
 
   const int seg = blockIdx.x;
   const int tid = threadIdx.x;
@@ -51,6 +54,16 @@ __global__ __launch_bounds__(T) void topk_select_kernel(TopkArgs a) {
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   uint16_t* keys = reinterpret_cast<uint16_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   const uint16_t* sc = a.score + start;
+
+  if (n <= T && k <= vtx::kMaxBitonicK) {  // uniform: one score per thread, the bitonic select
+    const int i = tid;
+    const uint16_t v = sc[i < n ? i : n - 1];  // (past n: position n - 1, not used)
+    const uint32_t comp = vtx::bitonic_comp(i < n, vtx::score_key(v), i);
+    vtx::select_bitonic<T>(comp, k, bsh, [&](int r, uint32_t c) {
+      a.sidx[obase + r] = a.didx[start + vtx::bitonic_position(c)];
+    });
+    return;
+  }
 
   if (n <= a.key_cap) {
     constexpr int kU = 4;  // score loads in flight per thread
@@ -121,7 +134,9 @@ extern "C" int vtx_topk_select(const uint16_t* score, int64_t score_len,
   const size_t lds = (size_t)vtx::sel_slots(topk_val) * 8 + (size_t)cap * 2;
 
   hipStream_t s = vtx::as_stream(stream);
-  if (max_num_pages <= 512) {
+  // (up to 512 pages and k <= 32: 512 threads, one page each, for the
+  // bitonic select)
+  if (max_num_pages <= 256 || (max_num_pages <= 512 && topk_val > vtx::kMaxBitonicK)) {
     topk_select_kernel<256><<<eff_batch_size, 256, lds, s>>>(a);
   } else if (max_num_pages <= 2048) {
     topk_select_kernel<512><<<eff_batch_size, 512, lds, s>>>(a);
