@@ -526,6 +526,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T, kSplitHistCopies> sh;
+  __shared__ vtx::BitonicRunShared<T> bsr;  // the selecting workgroup's bitonic select
   __shared__ int s_last;
   __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
   __shared__ __align__(16) uint16_t fresh_row[cm_on && VPL > 1 ? kWaves * kMaxQueryDim : 8];  // per wave, CMean
@@ -696,6 +697,33 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
 
   // ---- top-k of the segment from the stored scores (device-coherent loads)
   const uint16_t* scs = a.score + start;
+  constexpr int kRunR = 4;  // scores per thread of the bitonic select
+  if (n <= (long long)T * kRunR && k <= vtx::kMaxBitonicRunK && n <= a.row_cap) {  // uniform
+    // thread t holds positions t * kRunR + u (past n: position n - 1 again,
+    // not an item); the row ids go to LDS by position for the emit
+    int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);
+    uint16_t v[kRunR];
+    int rid[kRunR];
+#pragma unroll
+    for (int u = 0; u < kRunR; ++u) {
+      const long long i = (long long)tid * kRunR + u;
+      const long long ic = i < n ? i : n - 1;
+      v[u] = load_coherent(scs + ic);
+      rid[u] = dseg[ic];
+    }
+    uint32_t comp[kRunR];
+#pragma unroll
+    for (int u = 0; u < kRunR; ++u) {
+      const long long i = (long long)tid * kRunR + u;
+      comp[u] = vtx::bitonic_comp(i < n, vtx::score_key(v[u]), (int)i);
+      rid_lds[i < n ? i : n - 1] = rid[u];
+    }
+    vtx::select_bitonic_run<T, kRunR>(comp, k, bsr, [&](int rank, uint32_t c) {
+      a.sidx[obase + rank] = rid_lds[vtx::bitonic_position(c)];
+    });
+    cm_tiles();
+    return;
+  }
   if (n <= (long long)T * kTailR) {  // uniform: every score and row id in registers
     // thread t holds positions t * kTailR + u: a thread's items are
     // consecutive, so one prefix over the lanes ranks the ties
@@ -1002,12 +1030,13 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     const long long fill = eff_batch_size > 0 ? resident / eff_batch_size : 1;
     if (cps > fill) cps = fill;
     if (cps < 1) cps = 1;
-    const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8 - (long long)a.topk * 4) / 2;
+    const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8 - (long long)a.topk * 4) / 6;
     long long cap = want < room ? want : room;
     cap &= ~7LL;
     if (cap < 0) cap = 0;
     a.row_cap = (int32_t)cap;
-    const size_t lds = (size_t)vtx::sel_slots(a.topk) * 8 + (size_t)a.topk * 4 + (size_t)cap * 2;  // sel, payloads, keys
+    // sel, payloads, keys, and the bitonic select's row ids by position
+    const size_t lds = (size_t)vtx::sel_slots(a.topk) * 8 + (size_t)a.topk * 4 + (size_t)cap * 6;
     long long items = (long long)eff_batch_size * cps + (a.x_out ? q_rows - eff_batch_size : 0);
     items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
     if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");

@@ -544,4 +544,112 @@ __device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShar
   if (wave == 0 && lane < k) emit(lane, v);
 }
 
+// ---------------------------------------------------------------------------
+// The bitonic select for kR items per lane and k <= 64 (the split layout's
+// selecting workgroup): lane l of a wave holds elements l * kR + u.  Each
+// wave sorts its 64 * kR composites descending (strides below kR inside a
+// lane, the others across lanes) and keeps its best 64; pairs of 64-lists are
+// merged with two elements per lane (element 2l + u; a list against a
+// reversed one is bitonic) until wave 0 holds the best 64 in order.
+constexpr int kMaxBitonicRunK = 64;
+
+template <int T>
+struct BitonicRunShared {
+  uint32_t cand[2][(T / kWave) * 64];
+};
+
+// Compare-exchange of the element pair (lo, hi = lo ^ j, lo with bit j
+// clear): the lower element keeps the maximum when keep_max.
+__device__ __forceinline__ void bitonic_cx(uint32_t& lo, uint32_t& hi, bool keep_max) {
+  const uint32_t a = lo > hi ? lo : hi, b = lo > hi ? hi : lo;
+  lo = keep_max ? a : b;
+  hi = keep_max ? b : a;
+}
+
+// The wave's 64 * kR values sorted descending (element lane * kR + u).
+template <int kR>
+__device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR]) {
+  constexpr int N = kWave * kR;
+  const int lane = lane_id();
+#pragma unroll
+  for (int k2 = 2; k2 <= N; k2 <<= 1)
+#pragma unroll
+    for (int j = k2 >> 1; j > 0; j >>= 1) {
+      if (j < kR) {
+#pragma unroll
+        for (int u = 0; u < kR; ++u)
+          if ((u & j) == 0) bitonic_cx(v[u], v[u | j], ((lane * kR + u) & k2) == 0);
+      } else {
+#pragma unroll
+        for (int u = 0; u < kR; ++u) {
+          const uint32_t o = xshfl_u32(v[u], j / kR);
+          const int e = lane * kR + u;
+          const bool keep_max = ((e & j) == 0) == ((e & k2) == 0);
+          v[u] = keep_max ? (v[u] > o ? v[u] : o) : (v[u] < o ? v[u] : o);
+        }
+      }
+    }
+}
+
+// A bitonic sequence of 128 values (element 2 * lane + u) sorted descending.
+__device__ __forceinline__ void wave_merge_desc2(uint32_t (&v)[2]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 2 * kWave / 2; j > 1; j >>= 1) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t o = xshfl_u32(v[u], j / 2);
+      v[u] = ((2 * lane + u) & j) == 0 ? (v[u] > o ? v[u] : o) : (v[u] < o ? v[u] : o);
+    }
+  }
+  bitonic_cx(v[0], v[1], true);
+}
+
+// The k (<= 64) best of the workgroup's composites, kR per thread (0: none):
+// emit(rank, comp) for rank 0 .. k-1, from wave 0.  Every thread of the
+// workgroup calls it; it contains barriers.
+template <int T, int kR, typename Emit>
+__device__ __forceinline__ void select_bitonic_run(uint32_t (&comp)[kR], int k, BitonicRunShared<T>& bs, Emit emit) {
+  static_assert(kR >= 1 && (kR & (kR - 1)) == 0 && 64 % kR == 0, "kR: a power of two dividing 64");
+  constexpr int kWaves = T / kWave;
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  wave_sort_desc_run<kR>(comp);
+  if constexpr (kWaves == 1) {
+#pragma unroll
+    for (int u = 0; u < kR; ++u)
+      if (lane * kR + u < k) emit(lane * kR + u, comp[u]);
+    return;
+  } else {
+    if (lane * kR < 64) {
+#pragma unroll
+      for (int u = 0; u < kR; ++u) bs.cand[0][wave * 64 + lane * kR + u] = comp[u];
+    }
+    uint32_t v[2] = {0u, 0u};
+    int buf = 0;
+#pragma unroll
+    for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 64 become w / 2
+      __syncthreads();
+      if (wave < w / 2) {  // uniform
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int e = 2 * lane + u;
+          v[u] = e < 64 ? bs.cand[buf][(2 * wave) * 64 + e] : bs.cand[buf][(2 * wave + 1) * 64 + (127 - e)];
+        }
+        wave_merge_desc2(v);
+        if (w > 2 && lane < 32) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) bs.cand[buf ^ 1][wave * 64 + 2 * lane + u] = v[u];
+        }
+      }
+      buf ^= 1;
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        if (2 * lane + u < k) emit(2 * lane + u, v[u]);
+    }
+  }
+}
+
 }  // namespace vtx
