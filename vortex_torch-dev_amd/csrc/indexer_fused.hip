@@ -699,14 +699,16 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   const uint16_t* scs = a.score + start;
   constexpr int kRunR = 4;  // scores per thread of the bitonic select
   if (n <= (long long)T * kRunR && k <= vtx::kMaxBitonicRunK && n <= a.row_cap) {  // uniform
-    // thread t holds positions t * kRunR + u (past n: position n - 1 again,
-    // not an item); the row ids go to LDS by position for the emit
+    // thread t holds positions u * T + t (each load coalesced across the
+    // workgroup; the sort takes its items in any order, each composite
+    // carries its position), past n: position n - 1 again, not an item; the
+    // row ids go to LDS by position for the emit
     int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);
     uint16_t v[kRunR];
     int rid[kRunR];
 #pragma unroll
     for (int u = 0; u < kRunR; ++u) {
-      const long long i = (long long)tid * kRunR + u;
+      const long long i = (long long)u * T + tid;
       const long long ic = i < n ? i : n - 1;
       v[u] = load_coherent(scs + ic);
       rid[u] = dseg[ic];
@@ -714,7 +716,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
     uint32_t comp[kRunR];
 #pragma unroll
     for (int u = 0; u < kRunR; ++u) {
-      const long long i = (long long)tid * kRunR + u;
+      const long long i = (long long)u * T + tid;
       comp[u] = vtx::bitonic_comp(i < n, vtx::score_key(v[u]), (int)i);
       rid_lds[i < n ? i : n - 1] = rid[u];
     }
