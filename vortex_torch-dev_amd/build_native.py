@@ -32,6 +32,10 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading pointer and integer kernel arguments (up to eight) are preloaded
+    # into SGPRs by the dispatch, so a kernel's first loads need no
+    # kernel-argument round trip (arguments after a by-value struct are not).
+    "-mllvm", "-amdgpu-kernarg-preload-count=8",
 ]
 
 

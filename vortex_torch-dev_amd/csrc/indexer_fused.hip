@@ -193,8 +193,17 @@ __device__ __forceinline__ void query_row(const FusedArgs& a, const vtx::U4 (&qv
 // stays in the register of the lane that produced it and the selection runs
 // on those registers (vtx::select_regs); longer segments keep their keys in
 // LDS (or re-read their stored scores) and use vtx::select_topk_counted.
+//
+// The operands of the first loads (the schedule, loc and their sizes) come
+// again as leading scalar arguments, ahead of the argument structs: the
+// build preloads leading scalar kernel arguments into SGPRs
+// (-amdgpu-kernarg-preload-count), so these loads issue with the wave's
+// first instructions rather than after a kernel-argument round trip.
 template <int T, int LPR, int VPL, int kCmRegs>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(FusedArgs a, vtx::CmArgs cma) {
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(const int32_t* sched,
+                                                                               const int64_t* loc,
+                                                                               int32_t segments, int32_t loc_n,
+                                                                               FusedArgs a, vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   constexpr int kPass = vtx::segment_pass<VPL>();
@@ -221,7 +230,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   // ---- 0. with the in-kernel CMean, loc (issued first, so that waiting for
   // it waits for nothing else)
   long long cm_pos[kLocRegs];
-  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
+  if constexpr (cm_on) vtx::closing_load(loc, loc_n, cm_pos);
 
   // ---- 1. this workgroup's segment and its bounds: from the planner's
   // schedule when its header names this launch (the bounds it holds are a
@@ -231,26 +240,26 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(Fu
   bool predicted = false;
   int tile_rank = blockIdx.x;  // this workgroup's share of the CMean tiles
   int32_t pe[3] = {0, 0, 0};   // predicted dense begin, dense end, sparse begin
-  if (a.sched) {               // uniform
+  if (sched) {                 // uniform
     // header and entry loaded together, before any is looked at (one round
     // trip); workgroups past the segments read the last entry and ignore it
-    const bool mine = (int)blockIdx.x < a.segments;
-    const int32_t* e = a.sched + 4 + 4 * (long long)(mine ? blockIdx.x : a.segments - 1);
-    const int32_t h0 = a.sched[0], h1 = a.sched[1], h2 = a.sched[2];
+    const bool mine = (int)blockIdx.x < segments;
+    const int32_t* e = sched + 4 + 4 * (long long)(mine ? blockIdx.x : segments - 1);
+    const int32_t h0 = sched[0], h1 = sched[1], h2 = sched[2];
     const int32_t e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3];
-    const bool ok = (h0 == vtx::kSchedMagic) & (h1 == a.segments) & (h2 >= 1);
-    if (mine) {
-      pe[0] = e1;
-      pe[1] = e2;
-      pe[2] = e3;
-      if (ok && e0 >= 0 && e0 < a.segments) {
-        seg = e0;
-        predicted = true;
-      }
-    }
-    if (ok) tile_rank = vtx::sched_short_rank32(blockIdx.x, (uint32_t)a.segments, (uint32_t)h2);
+    const bool ok = (h0 == vtx::kSchedMagic) & (h1 == segments) & (h2 >= 1);
+    // selects, not branches: a load whose value is used only inside a branch
+    // is moved into it, and the entry would then wait for the header
+    predicted = mine & ok & (e0 >= 0) & (e0 < segments);
+    seg = predicted ? e0 : seg;
+    pe[0] = e1;  // read only when predicted
+    pe[1] = e2;
+    pe[2] = e3;
+    const int32_t rounds = h2 >= 1 ? h2 : 1;
+    const int rank = vtx::sched_short_rank32(blockIdx.x, (uint32_t)segments, (uint32_t)rounds);
+    tile_rank = ok ? rank : tile_rank;
   }
-  const bool is_seg = seg < a.segments;
+  const bool is_seg = seg < segments;
   long long start = 0, n = 0, obase = 0;
   if (predicted) {
     start = (long long)pe[0] + a.bos;
@@ -514,9 +523,16 @@ constexpr int kSplitHistCopies = 8;
 // centroid the launch rewrites is scored against the centroid recomputed
 // from its K tile (reduced into the wave's LDS row, read back in the scoring
 // layout).
+//
+// As in indexer_fused_kernel, the operands of the first loads (the block
+// tables' bounds, loc and the sizes the work id needs, gridDim.x / 8
+// included: the grid size is itself a kernel argument) lead the argument
+// list, so that they are preloaded into SGPRs.
 template <int T, int LPR, int VPL, int kPass, int kCmRegs>
-__global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* counters, int32_t cps,
-                                                          vtx::CmArgs cma) {
+__global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr, const int32_t* sindptr,
+                                                          const int64_t* loc, int32_t segments, int32_t loc_n,
+                                                          int32_t cps, int32_t per_xcd, FusedArgs a,
+                                                          int32_t* counters, vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   constexpr int kChunk = kWaves * kPass;
@@ -540,10 +556,11 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   const int D = a.dim;
 
   long long cm_pos[kLocRegs];
-  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
-  const long long per_xcd = gridDim.x / 8;  // the host rounds the grid to a multiple of 8
+  if constexpr (cm_on) vtx::closing_load(loc, loc_n, cm_pos);
+  // per_xcd = gridDim.x / 8 (the host rounds the grid to a multiple of 8),
+  // passed so that the work id waits for no kernel-argument load
   const long long w = (long long)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  const long long chunk_items = (long long)a.segments * cps;
+  const long long chunk_items = (long long)segments * cps;
   vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
   // the closed pages of loc (waits for the loc loads: called once the
@@ -566,7 +583,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   vtx::U4 qv[kQRegs][VPL];
   if (w >= chunk_items) {  // query rows past the segments: only their mean
     build_closing();
-    const long long row = a.segments + (w - chunk_items);
+    const long long row = segments + (w - chunk_items);
     if (a.x_out && a.G > 0 && row < a.q_rows) {
       if (a.G <= kQRegs)
         query_row<LPR, VPL, kQRegs>(a, qv, false, a.q + row * a.G * D, (int)row, wave == 0 && grp == 0, col, xs);
@@ -583,7 +600,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(FusedArgs a, int32_t* 
   // the segment's bounds in one vector load (lane 0: dense begin, lane 1:
   // dense end, lane 2: sparse begin; one round trip, where three scalar-path
   // loads would each wait for the one before)
-  const int32_t* bp = lane == 1 ? a.dindptr + seg + 1 : lane == 2 ? a.sindptr + seg : a.dindptr + seg;
+  const int32_t* bp = lane == 1 ? dindptr + seg + 1 : lane == 2 ? sindptr + seg : dindptr + seg;
   const int32_t bv = *bp;
   const bool q_in_regs = a.G > 0 && a.G <= kQRegs;
   const uint16_t* qb = a.G > 0 ? a.q + (long long)seg * a.G * D : a.x + (long long)seg * D;
@@ -789,28 +806,41 @@ int launch_dim(const FusedArgs& a, const vtx::CmArgs* cm, int blocks, size_t lds
   const vtx::CmArgs none{};
   if (cm) {  // the in-kernel CMean: rows of one 16-byte vector per lane
     const bool one = cm->nnz <= vtx::kWave;  // loc in one register per lane
+    const int32_t nnz = (int32_t)cm->nnz;   // at most vtx::kCmLoc
     switch (a.dim) {
       case 64:
-        if (one) indexer_fused_kernel<T, 8, 1, 1><<<blocks, T, lds, s>>>(a, *cm);
-        else indexer_fused_kernel<T, 8, 1, vtx::kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
+        if (one) indexer_fused_kernel<T, 8, 1, 1>
+            <<<blocks, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
+        else indexer_fused_kernel<T, 8, 1, vtx::kCmLoc / vtx::kWave>
+            <<<blocks, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
         break;
       case 128:
-        if (one) indexer_fused_kernel<T, 16, 1, 1><<<blocks, T, lds, s>>>(a, *cm);
-        else indexer_fused_kernel<T, 16, 1, vtx::kCmLoc / vtx::kWave><<<blocks, T, lds, s>>>(a, *cm);
+        if (one) indexer_fused_kernel<T, 16, 1, 1>
+            <<<blocks, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
+        else indexer_fused_kernel<T, 16, 1, vtx::kCmLoc / vtx::kWave>
+            <<<blocks, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
         break;
       default: return vtx::fail(VTX_E_INVALID, "indexer_fused: in-kernel CMean needs head_dim 64 or 128");
     }
     return vtx::check_launch("indexer_fused (with CMean)");
   }
   switch (a.dim) {
-    case 64: indexer_fused_kernel<T, 8, 1, 0><<<blocks, T, lds, s>>>(a, none); break;
-    case 128: indexer_fused_kernel<T, 16, 1, 0><<<blocks, T, lds, s>>>(a, none); break;
-    case 256: indexer_fused_kernel<T, 16, 2, 0><<<blocks, T, lds, s>>>(a, none); break;
+    case 64:
+      indexer_fused_kernel<T, 8, 1, 0><<<blocks, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 128:
+      indexer_fused_kernel<T, 16, 1, 0><<<blocks, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 256:
+      indexer_fused_kernel<T, 16, 2, 0><<<blocks, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
     case 512:
-      if constexpr (T <= 512) indexer_fused_kernel<T, 16, 4, 0><<<blocks, T, lds, s>>>(a, none);
+      if constexpr (T <= 512)
+        indexer_fused_kernel<T, 16, 4, 0><<<blocks, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
       break;
     case 576:
-      if constexpr (T <= 512) indexer_fused_kernel<T, 8, 9, 0><<<blocks, T, lds, s>>>(a, none);
+      if constexpr (T <= 512)
+        indexer_fused_kernel<T, 8, 9, 0><<<blocks, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
       break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
@@ -832,12 +862,29 @@ int split_chunk(int dim, bool large) { return (split_threads(dim) / 64) * split_
 template <int P, int kCm>
 int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
                     const vtx::CmArgs& cm) {
+  const int32_t nnz = (int32_t)cm.nnz;  // at most vtx::kCmLoc with the CMean, else 0
+  const int32_t xcd = blocks / 8;       // work ids per XCD (blocks is a multiple of 8)
   switch (a.dim) {
-    case 64: indexer_split_kernel<512, 8, 1, 2 * P, kCm><<<blocks, 512, lds, s>>>(a, counters, cps, cm); break;
-    case 128: indexer_split_kernel<512, 16, 1, 2 * P, kCm><<<blocks, 512, lds, s>>>(a, counters, cps, cm); break;
-    case 256: indexer_split_kernel<512, 16, 2, P, kCm><<<blocks, 512, lds, s>>>(a, counters, cps, cm); break;
-    case 512: indexer_split_kernel<256, 16, 4, P, kCm><<<blocks, 256, lds, s>>>(a, counters, cps, cm); break;
-    case 576: indexer_split_kernel<256, 8, 9, P, kCm><<<blocks, 256, lds, s>>>(a, counters, cps, cm); break;
+    case 64:
+      indexer_split_kernel<512, 8, 1, 2 * P, kCm>
+          <<<blocks, 512, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+      break;
+    case 128:
+      indexer_split_kernel<512, 16, 1, 2 * P, kCm>
+          <<<blocks, 512, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+      break;
+    case 256:
+      indexer_split_kernel<512, 16, 2, P, kCm>
+          <<<blocks, 512, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+      break;
+    case 512:
+      indexer_split_kernel<256, 16, 4, P, kCm>
+          <<<blocks, 256, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+      break;
+    case 576:
+      indexer_split_kernel<256, 8, 9, P, kCm>
+          <<<blocks, 256, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+      break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch(kCm ? "indexer_fused (split, with CMean)" : "indexer_fused (split)");

@@ -46,13 +46,18 @@ struct Closing {
 // Issues the loads of loc (first in a kernel, so that waiting for them
 // waits for nothing else).
 template <int kLocRegs>
-__device__ __forceinline__ void closing_load(const CmArgs& cm, long long (&pos)[kLocRegs]) {
+__device__ __forceinline__ void closing_load(const int64_t* loc, long long nnz, long long (&pos)[kLocRegs]) {
   const int lane = lane_id();
 #pragma unroll
   for (int j = 0; j < kLocRegs; ++j) {
     const long long e = (long long)j * kWave + lane;
-    pos[j] = e < cm.nnz ? cm.loc[e] : 0;
+    pos[j] = e < nnz ? loc[e] : 0;
   }
+}
+
+template <int kLocRegs>
+__device__ __forceinline__ void closing_load(const CmArgs& cm, long long (&pos)[kLocRegs]) {
+  closing_load(cm.loc, cm.nnz, pos);
 }
 
 template <int kLocRegs>
