@@ -316,17 +316,23 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
       my_row = lane < cnt ? a.didx[start + p0 + lane] : -1;
     }
   };
+  // The row ids, then the segment's bounds from the block tables (the check
+  // of the prediction: one vector load, lane 0 dense begin, lane 1 dense
+  // end, lane 2 sparse begin) are requested before the barrier, and nothing
+  // waits for them before it: both come back in one round trip, and the
+  // barrier does not hold a wave whose loads are back for the others'.
+  if (active) first_pass();  // uniform
+  const int32_t* bp = lane == 1 ? a.dindptr + seg + 1 : lane == 2 ? a.sindptr + seg : a.dindptr + seg;
+  const int32_t bv = predicted ? *bp : 0;
   if (active) {  // uniform
     vtx::select_init<T>(sel, k, sh);
     __syncthreads();  // histogram cleared before any wave counts into it
-    first_pass();
   }
-  // the segment's bounds from the block tables, in the same round trip
-  int32_t tb[3] = {0, 0, 0};
-  if (predicted) {
-    tb[0] = a.dindptr[seg];
-    tb[1] = a.dindptr[seg + 1];
-    tb[2] = a.sindptr[seg];
+  int32_t tb[3] = {pe[0], pe[1], pe[2]};
+  if (predicted) {  // uniform
+    tb[0] = __builtin_amdgcn_readlane(bv, 0);
+    tb[1] = __builtin_amdgcn_readlane(bv, 1);
+    tb[2] = __builtin_amdgcn_readlane(bv, 2);
   }
   // The pages this launch's CMean closes (its tiles are reduced at the end
   // of the workgroup, see cm_tiles)
@@ -346,7 +352,8 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
       vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + tile_rank,
                                                        kWaves * (int)gridDim.x, grp, col);
   };
-  if (predicted && (tb[0] != pe[0] || tb[1] != pe[1] || tb[2] != pe[2])) {  // uniform; not for a current schedule
+  // (bitwise, not short-circuit: a load behind || would wait for the others)
+  if (predicted & ((tb[0] != pe[0]) | (tb[1] != pe[1]) | (tb[2] != pe[2]))) {  // uniform; not for a current schedule
     const bool was_active = active;
     start = (long long)tb[0] + a.bos;
     n = (long long)tb[1] - a.eos - start;
