@@ -324,7 +324,14 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
   if (active) first_pass();  // uniform
   const int32_t* bp = lane == 1 ? a.dindptr + seg + 1 : lane == 2 ? a.sindptr + seg : a.dindptr + seg;
   const int32_t bv = predicted ? *bp : 0;
-  if (active) {  // uniform
+  // The radix selects count into the LDS histogram, which is cleared first
+  // (one barrier); the bitonic select of one-pass segments counts nothing,
+  // so there the waves go on to their rows without waiting for each other.
+  auto needs_hist = [&]() {
+    return !(kRegSelect && n <= (long long)kWaves * kPass && k <= vtx::kMaxBitonicK && n <= a.row_cap);
+  };
+  bool hist = active && needs_hist();  // uniform
+  if (hist) {
     vtx::select_init<T>(sel, k, sh);
     __syncthreads();  // histogram cleared before any wave counts into it
   }
@@ -354,15 +361,15 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
   };
   // (bitwise, not short-circuit: a load behind || would wait for the others)
   if (predicted & ((tb[0] != pe[0]) | (tb[1] != pe[1]) | (tb[2] != pe[2]))) {  // uniform; not for a current schedule
-    const bool was_active = active;
     start = (long long)tb[0] + a.bos;
     n = (long long)tb[1] - a.eos - start;
     obase = (long long)tb[2] + a.bos;
     active = is_active();
     if (active) {
-      if (!was_active) {
+      if (!hist && needs_hist()) {
         vtx::select_init<T>(sel, k, sh);
         __syncthreads();
+        hist = true;
       }
       first_pass();
     }
