@@ -74,46 +74,68 @@ constexpr int kMaxQueryDim = 576;  // the widest supported head_dim
 // torch.mean(dim=1)'s order (its reduction over a strided dimension keeps
 // four fp32 accumulators, row g going to accumulator g % 4 in increasing g,
 // each starting from 0, combined as ((a0 + a1) + a2) + a3, then times the
-// factor inv_g; one thread reduces a whole column up to 16 rows): thread
-// t < D / 8 forms 16-byte column vector t into qm (LDS row of D bf16) and,
-// when `store`, into x_out row `row`.  No barrier.
+// factor inv_g), into qm (LDS row of D bf16) and, when `store`, into x_out
+// row `row`.  Two threads share 16-byte column vector c < D / 8: thread c
+// keeps accumulators 0 and 1, thread D / 8 + c accumulators 2 and 3 and
+// hands them over through `part` (LDS, D / 8 x 16 floats); each loads its 8
+// rows of a round of 16 before adding any, so up to 16 rows take one memory
+// round trip.  Every thread of the workgroup calls it (it holds a barrier);
+// qm is complete after the caller's next barrier.
+constexpr int kMeanRowsIn = 8;  // rows per thread loaded before any is added
+
 __device__ __forceinline__ void query_mean_lds(const FusedArgs& a, const uint16_t* qb, int row, bool store,
-                                               uint16_t* qm) {
-  constexpr int kRowsIn = 8;  // rows loaded before any is added
+                                               uint16_t* qm, float (*part)[16]) {
   const int D = a.dim;
   const int nv = D / 8;
-  for (int t = threadIdx.x; t < nv; t += blockDim.x) {
-    float acc[4][8];
+  for (int base = 0; base < 2 * nv; base += blockDim.x) {  // the same trip count in every thread
+    const int t = base + (int)threadIdx.x;
+    const bool on = t < 2 * nv;
+    const int h = t < nv ? 0 : 1;  // accumulators 2h, 2h + 1
+    const int c = on ? t - h * nv : 0;
+    float acc[2][8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-    for (int g0 = 0; g0 < a.G; g0 += kRowsIn) {
-      // every load issued before any add (rows past G re-read row G - 1 and
-      // are not added), with constant register indices throughout
-      vtx::U4 r[kRowsIn];
+    if (on) {
+      for (int g0 = 0; g0 < a.G; g0 += 2 * kMeanRowsIn) {
+        // row g0 + 4 (j / 2) + 2h + j % 2 goes to accumulator j % 2; rows
+        // past G re-read row G - 1 and are not added (a select, not a
+        // branch, which would let the compiler wait for each row alone)
+        vtx::U4 r[kMeanRowsIn];
 #pragma unroll
-      for (int j = 0; j < kRowsIn; ++j) {
-        const int g = g0 + j < a.G ? g0 + j : a.G - 1;
-        r[j] = vtx::ld16(qb + (long long)g * D + t * 8);
+        for (int j = 0; j < kMeanRowsIn; ++j) {
+          const int g = g0 + 4 * (j / 2) + 2 * h + j % 2;
+          r[j] = vtx::ld16(qb + (long long)(g < a.G ? g : a.G - 1) * D + c * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < kMeanRowsIn; ++j) {
+          const bool in = g0 + 4 * (j / 2) + 2 * h + j % 2 < a.G;
+          float f[8];
+          vtx::unpack8(r[j], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j % 2][e] = in ? acc[j % 2][e] + f[e] : acc[j % 2][e];
+        }
       }
+      if (h == 1) {
 #pragma unroll
-      for (int j = 0; j < kRowsIn; ++j) {
-        // a select, not a branch (a branch lets the compiler sink the load
-        // into it and wait for each row on its own)
-        const bool in = g0 + j < a.G;
-        float f[8];
-        vtx::unpack8(r[j], f);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j % 4][e] = in ? acc[j % 4][e] + f[e] : acc[j % 4][e];
+        for (int e = 0; e < 8; ++e) {
+          part[c][e] = acc[0][e];
+          part[c][8 + e] = acc[1][e];
+        }
       }
     }
-    uint32_t b[8];
+    __syncthreads();
+    if (on && h == 0) {
+      uint32_t b[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) b[e] = vtx::f32_to_bf16((((acc[0][e] + acc[1][e]) + acc[2][e]) + acc[3][e]) * a.inv_g);
-    const vtx::U4 m{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
-    vtx::st16(qm + t * 8, m);
-    if (store && a.x_out) vtx::st16(a.x_out + (long long)row * D + t * 8, m);
+      for (int e = 0; e < 8; ++e)
+        b[e] = vtx::f32_to_bf16((((acc[0][e] + acc[1][e]) + part[c][e]) + part[c][8 + e]) * a.inv_g);
+      const vtx::U4 m{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+      vtx::st16(qm + c * 8, m);
+      if (store && a.x_out) vtx::st16(a.x_out + (long long)row * D + c * 8, m);
+    }
+    if (base + (int)blockDim.x < 2 * nv) __syncthreads();  // `part` is read before the next round writes it
   }
 }
 
@@ -214,6 +236,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
   __shared__ vtx::SelectShared<T> sh;
   __shared__ vtx::BitonicShared<T> bsh;  // kRegSelect with k <= 32: the bitonic select
   __shared__ __align__(16) uint16_t qm_row[VPL * LPR * 8];  // query mean, G > kQRegs
+  __shared__ float qm_part[VPL * LPR][16];                   // its second half's accumulators
 
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
@@ -377,7 +400,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
   if (!active) {
     if (a.x_out) {
       if (q_in_regs) query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-      else query_mean_lds(a, qb, seg, true, qm_row);
+      else query_mean_lds(a, qb, seg, true, qm_row, qm_part);
     }
     cm_tiles();
     return;
@@ -387,7 +410,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
 
   bool have_mean = false;
   if (!q_in_regs) {  // (more than kQRegs rows to average: formed in LDS, before the loop)
-    query_mean_lds(a, qb, seg, true, qm_row);
+    query_mean_lds(a, qb, seg, true, qm_row, qm_part);
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < VPL; ++v) vtx::unpack8(vtx::ld16(qm_row + (v * LPR + col) * 8), xs[v]);
@@ -559,6 +582,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   __shared__ vtx::BitonicRunShared<T> bsr;  // the selecting workgroup's bitonic select
   __shared__ int s_last;
   __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
+  __shared__ float qm_part[VPL * LPR][16];                                     // its second half's accumulators
   __shared__ __align__(16) uint16_t fresh_row[cm_on && VPL > 1 ? kWaves * kMaxQueryDim : 8];  // per wave, CMean
 
   const int tid = threadIdx.x;
@@ -602,7 +626,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
       if (a.G <= kQRegs)
         query_row<LPR, VPL, kQRegs>(a, qv, false, a.q + row * a.G * D, (int)row, wave == 0 && grp == 0, col, xs);
       else
-        query_mean_lds(a, a.q + row * a.G * D, (int)row, true, qm_row);
+        query_mean_lds(a, a.q + row * a.G * D, (int)row, true, qm_row, qm_part);
     }
     cm_tiles();
     return;
@@ -639,7 +663,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   const bool mean_in_lds = a.G > kQRegs;
   if (c >= workers) {  // nothing to score (or an inactive segment): only the mean
     if (c == 0 && a.x_out) {
-      if (mean_in_lds) query_mean_lds(a, qb, seg, true, qm_row);
+      if (mean_in_lds) query_mean_lds(a, qb, seg, true, qm_row, qm_part);
       else query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
     }
     cm_tiles();
@@ -653,7 +677,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   vtx::select_init<T>(sel, k, sh);
   const int32_t* dseg = a.didx + start;
   if (mean_in_lds) {  // workgroup-uniform
-    query_mean_lds(a, qb, seg, c == 0, qm_row);
+    query_mean_lds(a, qb, seg, c == 0, qm_row, qm_part);
     __syncthreads();
 #pragma unroll
     for (int v = 0; v < VPL; ++v) vtx::unpack8(vtx::ld16(qm_row + (v * LPR + col) * 8), xs[v]);
