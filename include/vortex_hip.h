@@ -299,6 +299,11 @@ int vtx_indexer_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_siz
  * (q_rows >= eff_batch_size * group_size); y: bf16 [y_rows, head_dim];
  * score_rows = pages of score ([score_rows, 1, group_size]); aggr_len =
  * pages of aggr.  group_size 1..8; topk_val <= 4096.
+ *
+ * schedule (optional, NULL for none): the fused_schedule vtx_plan_decode
+ * wrote for this block table, as for vtx_indexer_fused: the workgroups take
+ * the segments in its order and check the bounds it holds against the
+ * indptrs, so a schedule from an earlier plan only costs time.
  */
 int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                           const uint16_t* y, int64_t y_rows, int32_t head_dim,
@@ -308,7 +313,8 @@ int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                           int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                           int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                           int32_t reserved_eos, int32_t max_num_pages, int32_t softmax,
-                          float scale, void* stream);
+                          float scale, const int32_t* schedule, int64_t schedule_len,
+                          void* stream);
 
 /*
  * vtx_indexer_gqa_fused preceded by the layer's page-finish mean into y: the
@@ -330,7 +336,8 @@ int vtx_indexer_gqa_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group
                                 int32_t reserved_eos, int32_t max_num_pages, int32_t softmax,
                                 float scale, const uint16_t* k_cache, int64_t k_rows,
                                 int32_t page_size, int32_t num_kv_heads, const int64_t* loc,
-                                int64_t nnz, void* stream);
+                                int64_t nnz, const int32_t* schedule, int64_t schedule_len,
+                                void* stream);
 
 /* 1 if vtx_indexer_gqa_fused handles this head_dim and group size. */
 int vtx_indexer_gqa_fused_supported(int32_t head_dim, int32_t group_size);
@@ -355,6 +362,8 @@ int vtx_indexer_gqa_fused_supported(int32_t head_dim, int32_t group_size);
  * q: bf16 [q_rows, head_dim] (q_rows >= eff_batch_size * group_size);
  * ymax, ymin: bf16 [y_rows, head_dim]; sum_rows = pages of sum
  * ([sum_rows, group_size, 1]); group_size 1..8; topk_val <= 4096.
+ * schedule (optional, NULL for none): the planner's fused_schedule, as for
+ * vtx_indexer_gqa_fused.
  */
 int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                             const uint16_t* ymax, const uint16_t* ymin, int64_t y_rows,
@@ -364,7 +373,8 @@ int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_t group_siz
                             const int32_t* dense_kv_indices, int64_t dense_kv_indices_len,
                             int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                             int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
-                            int32_t reserved_eos, int32_t max_num_pages, void* stream);
+                            int32_t reserved_eos, int32_t max_num_pages,
+                            const int32_t* schedule, int64_t schedule_len, void* stream);
 
 /*
  * vtx_indexer_quest_fused preceded by the layer's CMax + CMin into ymax and
@@ -386,7 +396,8 @@ int vtx_indexer_quest_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t gro
                                   int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                                   int32_t reserved_eos, int32_t max_num_pages, const uint16_t* k_cache,
                                   int64_t k_rows, int32_t page_size, int32_t num_kv_heads,
-                                  const int64_t* loc, int64_t nnz, void* stream);
+                                  const int64_t* loc, int64_t nnz, const int32_t* schedule,
+                                  int64_t schedule_len, void* stream);
 
 /* 1 if vtx_indexer_quest_fused handles this head_dim and group size. */
 int vtx_indexer_quest_fused_supported(int32_t head_dim, int32_t group_size);

@@ -149,3 +149,123 @@ def test_fused_schedule_without_header_is_ignored(gpu):
     junk = torch.randint(0, S, (4 + 4 * S,), dtype=torch.int32, generator=torch.Generator().manual_seed(3)).to(dev)
     junk[0] = 0  # no header
     _equal(_fused(batch, ic, dev, junk), _fused(batch, ic, dev, None))
+
+
+def _gqa(batch, ic, dev, schedule, cmean=False, softmax=True, seed=1):
+    """The fused GQA indexer step (GeMM, softmax, max, topK) on one layer."""
+    H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+    S = batch.batch * H
+    q = W.randn_bf16((S, G, D), seed, dev)
+    rows = batch.pool_pages * H
+    y = W.randn_bf16((rows, 1, D), seed + 1, dev, std=0.25)
+    pages = ic.dense_kv_indices.numel()
+    sc = torch.full((pages, 1, G), -5.0, device=dev, dtype=torch.bfloat16)
+    ag = torch.full((pages, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
+    sp = ic.sparse_kv_indices.clone()
+    cm = None
+    if cmean:
+        k = W.randn_bf16((rows, batch.page_size, D), seed + 2, dev)
+        cm = (k, W.decode_loc(batch).to(dev), H)
+    _hip.indexer_gqa_fused(q, y, sc, ag, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp, S,
+                           batch.topk, batch.bos, batch.eos, batch.max_pages_per_request,
+                           softmax_scale=D ** -0.5 if softmax else None, cmean=cm, schedule=schedule)
+    torch.cuda.synchronize()
+    return [sc, ag, sp, y]
+
+
+def _gqa_batch(name):
+    batch = _batches()[name]()
+    if not _hip.indexer_gqa_fused_supported(batch.head_dim, batch.group_size):
+        pytest.skip(f"the fused GQA kernel does not serve D {batch.head_dim}, G {batch.group_size}")
+    return batch
+
+
+@pytest.mark.parametrize("softmax", [False, True])
+@pytest.mark.parametrize("cmean", [False, True])
+@pytest.mark.parametrize("name", ["c1", "c2", "r3", "r5", "r9"])
+def test_gqa_fused_with_schedule_equals_without(gpu, name, cmean, softmax):
+    dev = gpu
+    batch = _gqa_batch(name)
+    if cmean and batch.head_dim not in (64, 128):
+        pytest.skip("the in-launch CMean serves head_dim 64 / 128")
+    S = batch.batch * batch.num_kv_heads
+    sched = torch.zeros((4 + 4 * S,), dtype=torch.int32, device=dev)
+    ic = _plan(batch, dev, sched, 7)
+    _equal(_gqa(batch, ic, dev, sched, cmean, softmax), _gqa(batch, ic, dev, None, cmean, softmax))
+
+
+@pytest.mark.parametrize("cmean", [False, True])
+def test_gqa_fused_with_stale_schedule_is_still_exact(gpu, cmean):
+    dev = gpu
+    a, b = W.c2(seed=1), W.c2(seed=5)
+    S = a.batch * a.num_kv_heads
+    sched = torch.zeros((4 + 4 * S,), dtype=torch.int32, device=dev)
+    _plan(a, dev, sched)
+    ic_b = _plan(b, dev, None)
+    assert int(sched[0]) == MAGIC
+    _equal(_gqa(b, ic_b, dev, sched, cmean), _gqa(b, ic_b, dev, None, cmean))
+
+
+def test_gqa_fused_schedule_without_header_is_ignored(gpu):
+    dev = gpu
+    batch = W.c2()
+    S = batch.batch * batch.num_kv_heads
+    ic = _plan(batch, dev)
+    junk = torch.randint(0, S, (4 + 4 * S,), dtype=torch.int32, generator=torch.Generator().manual_seed(3)).to(dev)
+    junk[0] = 0
+    _equal(_gqa(batch, ic, dev, junk), _gqa(batch, ic, dev, None))
+
+
+def _quest(batch, ic, dev, schedule, envelope=False, seed=1):
+    """The fused Quest indexer step (envelope scores, max, topK) on one layer."""
+    H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+    S = batch.batch * H
+    q = W.randn_bf16((S, G, D), seed, dev)
+    rows = batch.pool_pages * H
+    ymax = W.randn_bf16((rows, 1, D), seed + 1, dev, std=0.25)
+    ymin = W.randn_bf16((rows, 1, D), seed + 3, dev, std=0.25)
+    pages = ic.dense_kv_indices.numel()
+    sm = torch.full((pages, G, 1), -5.0, device=dev, dtype=torch.bfloat16)
+    ag = torch.full((pages, 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
+    sp = ic.sparse_kv_indices.clone()
+    env = None
+    if envelope:
+        k = W.randn_bf16((rows, batch.page_size, D), seed + 2, dev)
+        env = (k, W.decode_loc(batch).to(dev), H)
+    _hip.indexer_quest_fused(q, ymax, ymin, sm, ag, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices,
+                             sp, S, batch.topk, batch.bos, batch.eos, batch.max_pages_per_request, envelope=env,
+                             schedule=schedule)
+    torch.cuda.synchronize()
+    return [sm, ag, sp, ymax, ymin]
+
+
+def _quest_batch(name):
+    batch = _batches()[name]()
+    if not _hip.indexer_quest_fused_supported(batch.head_dim, batch.group_size):
+        pytest.skip(f"the fused Quest kernel does not serve D {batch.head_dim}, G {batch.group_size}")
+    return batch
+
+
+@pytest.mark.parametrize("envelope", [False, True])
+@pytest.mark.parametrize("name", ["c1", "c2", "r3", "r5", "r9"])
+def test_quest_fused_with_schedule_equals_without(gpu, name, envelope):
+    dev = gpu
+    batch = _quest_batch(name)
+    if envelope and batch.head_dim not in (64, 128):
+        pytest.skip("the in-launch page reduce serves head_dim 64 / 128")
+    S = batch.batch * batch.num_kv_heads
+    sched = torch.zeros((4 + 4 * S,), dtype=torch.int32, device=dev)
+    ic = _plan(batch, dev, sched, 7)
+    _equal(_quest(batch, ic, dev, sched, envelope), _quest(batch, ic, dev, None, envelope))
+
+
+@pytest.mark.parametrize("envelope", [False, True])
+def test_quest_fused_with_stale_schedule_is_still_exact(gpu, envelope):
+    dev = gpu
+    a, b = W.c2(seed=1), W.c2(seed=5)
+    S = a.batch * a.num_kv_heads
+    sched = torch.zeros((4 + 4 * S,), dtype=torch.int32, device=dev)
+    _plan(a, dev, sched)
+    ic_b = _plan(b, dev, None)
+    assert int(sched[0]) == MAGIC
+    _equal(_quest(b, ic_b, dev, sched, envelope), _quest(b, ic_b, dev, None, envelope))

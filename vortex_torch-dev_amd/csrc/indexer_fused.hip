@@ -259,29 +259,11 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
   // schedule when its header names this launch (the bounds it holds are a
   // prediction, checked against the block tables below), else segment
   // blockIdx.x and the block tables
-  int seg = blockIdx.x;
-  bool predicted = false;
-  int tile_rank = blockIdx.x;  // this workgroup's share of the CMean tiles
-  int32_t pe[3] = {0, 0, 0};   // predicted dense begin, dense end, sparse begin
-  if (sched) {                 // uniform
-    // header and entry loaded together, before any is looked at (one round
-    // trip); workgroups past the segments read the last entry and ignore it
-    const bool mine = (int)blockIdx.x < segments;
-    const int32_t* e = sched + 4 + 4 * (long long)(mine ? blockIdx.x : segments - 1);
-    const int32_t h0 = sched[0], h1 = sched[1], h2 = sched[2];
-    const int32_t e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3];
-    const bool ok = (h0 == vtx::kSchedMagic) & (h1 == segments) & (h2 >= 1);
-    // selects, not branches: a load whose value is used only inside a branch
-    // is moved into it, and the entry would then wait for the header
-    predicted = mine & ok & (e0 >= 0) & (e0 < segments);
-    seg = predicted ? e0 : seg;
-    pe[0] = e1;  // read only when predicted
-    pe[1] = e2;
-    pe[2] = e3;
-    const int32_t rounds = h2 >= 1 ? h2 : 1;
-    const int rank = vtx::sched_short_rank32(blockIdx.x, (uint32_t)segments, (uint32_t)rounds);
-    tile_rank = ok ? rank : tile_rank;
-  }
+  const vtx::SchedPick pick = vtx::sched_pick(sched, segments);
+  const int seg = pick.seg;
+  const bool predicted = pick.predicted;
+  const int tile_rank = pick.tile_rank;  // this workgroup's share of the CMean tiles
+  const int32_t* pe = pick.pe;           // predicted dense begin, dense end, sparse begin
   const bool is_seg = seg < segments;
   long long start = 0, n = 0, obase = 0;
   if (predicted) {

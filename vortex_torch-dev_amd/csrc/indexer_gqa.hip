@@ -17,6 +17,7 @@
 // buffers.
 #include "vtx_cmean.h"
 #include "vtx_device.h"
+#include "vtx_fused_schedule.h"
 #include "vtx_host.h"
 #include "vtx_score.h"
 #include "vtx_segment.h"
@@ -41,14 +42,24 @@ struct GqaArgs {
   int32_t segments, G, dim, topk, bos, eos, row_cap;
   int32_t softmax;
   float scale;
+  const int32_t* sched;  // the planner's workgroup schedule, or null (passed to the kernel up front)
 };
 
 // kCmRegs > 0: the launch also runs the layer's decode CMean into y (loc: up
 // to 64 * kCmRegs entries, rows of one vector per lane), as the block-sparse
-// fused kernel does (vtx_cmean.h).
+// fused kernel does (vtx_cmean.h); its tiles go to the workgroups that finish
+// first, after their own select.
+//
+// With the planner's workgroup schedule (sched, vtx_fused_schedule.h) the
+// workgroups take the segments in its order, every compute unit a short and
+// a long one; the bounds it holds are checked against the block tables in
+// the round trip of the first row ids, before anything is written, so a
+// stale schedule costs time, never a result.  The schedule, loc and their
+// sizes lead the argument list, so that the dispatch preloads them into
+// SGPRs and the first loads wait for no kernel-argument load.
 template <int T, int LPR, int VPL, int kG, int kCmRegs>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fused_kernel(GqaArgs a,
-                                                                                       vtx::CmArgs cma) {
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fused_kernel(
+    const int32_t* sched, const int64_t* loc, int32_t segments, int32_t loc_n, GqaArgs a, vtx::CmArgs cma) {
   static_assert(T >= vtx::kScanThreads, "the softmax statistics need kScanThreads threads");
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
@@ -62,7 +73,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   constexpr bool cm_on = kCmRegs > 0 && VPL == 1;
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
 
-  const int seg = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
   const int wave = vtx::uniform(tid / vtx::kWave);
@@ -73,14 +83,56 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   const int G = a.G;
 
   long long cm_pos[kLocRegs];
-  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
-  const long long start = (long long)a.dindptr[seg] + a.bos;
-  const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
-  const long long obase = (long long)a.sindptr[seg] + a.bos;
-  const bool active = k > 0 && n > k && start >= 0 && start + n <= a.score_rows && start + n <= a.aggr_len &&
-                      start + n <= a.didx_len && obase >= 0 && obase + k <= a.sidx_len;
+  if constexpr (cm_on) vtx::closing_load(loc, loc_n, cm_pos);
+  const vtx::SchedPick pick = vtx::sched_pick(sched, segments);
+  const int seg = pick.seg;
+  long long start, n, obase;
+  if (pick.predicted) {
+    start = (long long)pick.pe[0] + a.bos;
+    n = (long long)pick.pe[1] - a.eos - start;
+    obase = (long long)pick.pe[2] + a.bos;
+  } else {
+    start = (long long)a.dindptr[seg] + a.bos;
+    n = (long long)a.dindptr[seg + 1] - a.eos - start;
+    obase = (long long)a.sindptr[seg] + a.bos;
+  }
+  auto is_active = [&]() {
+    return k > 0 && n > k && start >= 0 && start + n <= a.score_rows && start + n <= a.aggr_len &&
+           start + n <= a.didx_len && obase >= 0 && obase + k <= a.sidx_len;
+  };
+  bool active = is_active();
   if constexpr (!cm_on) {
-    if (!active) return;  // uniform: the separate ops write nothing for this segment either
+    if (!active && !pick.predicted) return;  // uniform: the separate ops write nothing for this segment either
+  }
+  // the first pass's row ids, then the check of the predicted bounds (one
+  // vector load: lane 0 dense begin, lane 1 dense end, lane 2 sparse
+  // begin), both in one round trip
+  long long share = 0;
+  int my_row = -1;
+  auto first_pass = [&]() {
+    share = (n + kWaves - 1) / kWaves;
+    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+    if (share > kPass) share = kPass;
+    const long long p0 = (long long)wave * share;
+    const long long cnt = p0 < n ? min(share, n - p0) : 0;
+    my_row = lane < cnt ? a.didx[start + p0 + lane] : -1;
+  };
+  if (active) first_pass();  // uniform
+  if (pick.predicted) {      // uniform
+    const int32_t* bp = lane == 1 ? a.dindptr + seg + 1 : lane == 2 ? a.sindptr + seg : a.dindptr + seg;
+    const int32_t bv = *bp;
+    const int32_t t0 = __builtin_amdgcn_readlane(bv, 0), t1 = __builtin_amdgcn_readlane(bv, 1),
+                  t2 = __builtin_amdgcn_readlane(bv, 2);
+    if ((t0 != pick.pe[0]) | (t1 != pick.pe[1]) | (t2 != pick.pe[2])) {  // uniform; not for a current schedule
+      start = (long long)t0 + a.bos;
+      n = (long long)t1 - a.eos - start;
+      obase = (long long)t2 + a.bos;
+      active = is_active();
+      if (active) first_pass();
+    }
+  }
+  if constexpr (!cm_on) {
+    if (!active) return;  // uniform
   }
   const bool cached = n <= a.row_cap;
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
@@ -92,21 +144,28 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   const uint16_t* qs = a.q + (long long)seg * G * D;
   vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
-  long long share = 0;
-  if (active) {  // uniform
-  vtx::select_init<T>(sel, k, sh);
   if constexpr (cm_on) {
     closing = vtx::closing_build(cma, cm_pos);
     n_close = closing.count;
   }
+  // this launch's CMean: wave w of the workgroup of tile rank r reduces tiles
+  // w * grid + r, ... once its own segment is done (rank 0: the shortest
+  // segment under a schedule)
+  auto cm_tiles = [&]() {
+    if constexpr (cm_on)
+      vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + pick.tile_rank,
+                                                       kWaves * (int)gridDim.x, grp, col);
+  };
+  if (!active) {  // uniform (only with the CMean)
+    cm_tiles();
+    return;
+  }
+  vtx::select_init<T>(sel, k, sh);
 
   // ---- scores of every middle page for every query head
-  share = (n + kWaves - 1) / kWaves;
-  share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
-  if (share > kPass) share = kPass;
   for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
     const int cnt = (int)min(share, n - p0);
-    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
+    if (p0 != (long long)wave * share) my_row = lane < cnt ? dseg[p0 + lane] : -1;  // later passes
     int r = -1;
     for (int g0 = 0; g0 < G; g0 += kG) {
       float xs[kG][VPL][8];
@@ -160,14 +219,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
       }
     }
   }
-  }  // active
-  // this launch's CMean: wave w of workgroup b reduces tiles w * grid + b, ...
-  if constexpr (cm_on) {
-    if (!active) closing = vtx::closing_build(cma, cm_pos);
-    vtx::cmean_tiles<LPR, kLocRegs, vtx::kCentroid>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x,
-                                    kWaves * (int)gridDim.x, grp, col);
-    if (!active) return;
-  }
   __syncthreads();
 
   // ---- softmax statistics of each query head over the segment, then the
@@ -210,6 +261,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     const int i = threadIdx.x;
     const uint32_t comp = vtx::bitonic_comp(i < n, i < n ? (uint32_t)keys[i] : 0u, i);
     vtx::select_bitonic<T>(comp, k, bsh, [&](int rk, uint32_t c) { a.sidx[obase + rk] = rows[vtx::bitonic_position(c)]; });
+    cm_tiles();
     return;
   }
   if (cached) {
@@ -219,6 +271,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     vtx::select_topk_counted<T>([&](long long i) { return vtx::score_key(ag[i]); }, n, k, sel, sh);
   }
   vtx::select_emit<T>(sel, k, n, [&](int rk, long long pos) { a.sidx[obase + rk] = cached ? rows[pos] : dseg[pos]; });
+  cm_tiles();
 }
 
 constexpr int kLdsBudget = 52 * 1024;  // dynamic LDS; the select tables and statistics take up to ~8 KB more
@@ -230,26 +283,42 @@ int launch_dim(const GqaArgs& a, const vtx::CmArgs* cm, int grid, size_t lds, hi
   const vtx::CmArgs none{};
   if (cm) {  // the in-kernel CMean: rows of one 16-byte vector per lane
     const bool one = cm->nnz <= vtx::kWave;
+    const int32_t nnz = (int32_t)cm->nnz;  // at most vtx::kCmLoc
     switch (a.dim) {
       case 64:
-        if (one) gqa_fused_kernel<T, 8, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
-        else gqa_fused_kernel<T, 8, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        if (one) gqa_fused_kernel<T, 8, 1, kG, 1>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
+        else gqa_fused_kernel<T, 8, 1, kG, vtx::kCmLoc / vtx::kWave>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
         break;
       case 128:
-        if (one) gqa_fused_kernel<T, 16, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
-        else gqa_fused_kernel<T, 16, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        if (one) gqa_fused_kernel<T, 16, 1, kG, 1>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
+        else gqa_fused_kernel<T, 16, 1, kG, vtx::kCmLoc / vtx::kWave>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
         break;
       default: return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused: in-kernel CMean needs head_dim 64 or 128");
     }
     return vtx::check_launch("indexer_gqa_fused (with CMean)");
   }
   switch (a.dim) {
-    case 64: gqa_fused_kernel<T, 8, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
-    case 128: gqa_fused_kernel<T, 16, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
-    case 256: gqa_fused_kernel<T, 16, 2, 1, 0><<<grid, T, lds, s>>>(a, none); break;
+    case 64:
+      gqa_fused_kernel<T, 8, 1, kG, 0><<<grid, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 128:
+      gqa_fused_kernel<T, 16, 1, kG, 0><<<grid, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 256:
+      gqa_fused_kernel<T, 16, 2, 1, 0><<<grid, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
     // wide rows keep their query slice in registers: fewer threads, no spills
-    case 512: gqa_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1, 0><<<grid, (T > 512 ? 512 : T), lds, s>>>(a, none); break;
-    case 576: gqa_fused_kernel<256, 8, 9, 1, 0><<<grid, 256, lds, s>>>(a, none); break;
+    case 512:
+      gqa_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1, 0>
+          <<<grid, (T > 512 ? 512 : T), lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 576:
+      gqa_fused_kernel<256, 8, 9, 1, 0><<<grid, 256, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_gqa_fused");
@@ -283,7 +352,8 @@ int gqa_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16
              const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
              int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
              int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
-             int32_t max_num_pages, int32_t softmax, float scale, const CmeanSpec* cms, void* stream);
+             int32_t max_num_pages, int32_t softmax, float scale, const CmeanSpec* cms,
+             const int32_t* schedule, int64_t schedule_len, void* stream);
 
 }  // namespace
 
@@ -294,12 +364,13 @@ extern "C" int vtx_indexer_gqa_fused(const uint16_t* q, int64_t q_rows, int32_t 
                                      int64_t dense_kv_indices_len, int32_t* sparse_kv_indices,
                                      int64_t sparse_kv_indices_len, int32_t eff_batch_size, int32_t topk_val,
                                      int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
-                                     int32_t softmax, float scale, void* stream) {
+                                     int32_t softmax, float scale, const int32_t* schedule,
+                                     int64_t schedule_len, void* stream) {
   vtx::clear_error();
   return gqa_impl(q, q_rows, group_size, y, y_rows, head_dim, score, score_rows, aggr, aggr_len, dense_kv_indptr,
                   sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices, sparse_kv_indices_len,
                   eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, softmax, scale, nullptr,
-                  stream);
+                  schedule, schedule_len, stream);
 }
 
 extern "C" int vtx_indexer_gqa_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size, uint16_t* y,
@@ -311,7 +382,8 @@ extern "C" int vtx_indexer_gqa_fused_cmean(const uint16_t* q, int64_t q_rows, in
                                            int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
                                            int32_t softmax, float scale, const uint16_t* k_cache, int64_t k_rows,
                                            int32_t page_size, int32_t num_kv_heads, const int64_t* loc,
-                                           int64_t nnz, void* stream) {
+                                           int64_t nnz, const int32_t* schedule, int64_t schedule_len,
+                                           void* stream) {
   vtx::clear_error();
   if (!k_cache || (nnz > 0 && !loc))
     return vtx::fail(VTX_E_INVALID, "indexer_gqa_fused_cmean: null K pool or loc");
@@ -320,7 +392,8 @@ extern "C" int vtx_indexer_gqa_fused_cmean(const uint16_t* q, int64_t q_rows, in
   const CmeanSpec cm{k_cache, k_rows, page_size, num_kv_heads, loc, nnz};
   return gqa_impl(q, q_rows, group_size, y, y_rows, head_dim, score, score_rows, aggr, aggr_len, dense_kv_indptr,
                   sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices, sparse_kv_indices_len,
-                  eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, softmax, scale, &cm, stream);
+                  eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, softmax, scale, &cm, schedule,
+                  schedule_len, stream);
 }
 
 namespace {
@@ -330,7 +403,8 @@ int gqa_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16
              const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
              int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
              int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
-             int32_t max_num_pages, int32_t softmax, float scale, const CmeanSpec* cms, void* stream) {
+             int32_t max_num_pages, int32_t softmax, float scale, const CmeanSpec* cms,
+             const int32_t* schedule, int64_t schedule_len, void* stream) {
   const char* what = "indexer_gqa_fused";
   if (eff_batch_size < 0 || reserved_bos < 0 || reserved_eos < 0)
     return vtx::fail(VTX_E_INVALID, "%s: negative size", what);
@@ -378,6 +452,9 @@ int gqa_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16
   a.eos = reserved_eos;
   a.softmax = softmax != 0;
   a.scale = scale;
+  // a schedule too short for this launch is not used (the kernel would also
+  // ignore one whose header names another segment count)
+  a.sched = schedule && schedule_len >= vtx::sched_len(1, eff_batch_size) ? schedule : nullptr;
   const long long want = max_num_pages > 0 ? max_num_pages : 0;
   const long long per = 4 + 2 + 2LL * group_size;  // page id, key, raw scores
   const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8) / per;

@@ -15,6 +15,7 @@
 // kernel's.  The [pages, G, D] products and their maximum are not written.
 #include "vtx_cmean.h"
 #include "vtx_device.h"
+#include "vtx_fused_schedule.h"
 #include "vtx_host.h"
 #include "vtx_score.h"
 #include "vtx_select.h"
@@ -37,6 +38,7 @@ struct QuestArgs {
   int32_t* sidx;
   int64_t sidx_len;
   int32_t segments, G, dim, topk, bos, eos, row_cap;
+  const int32_t* sched;  // the planner's workgroup schedule, or null (passed to the kernel up front)
 };
 
 // Quest score of one envelope (mx, mn: the lane's 16-byte column vector of
@@ -57,10 +59,15 @@ __device__ __forceinline__ float quest_vec(const vtx::U4& mx, const vtx::U4& mn,
 
 // kCmRegs > 0: the launch also runs the layer's CMax + CMin into the envelope
 // pools (loc: up to 64 * kCmRegs entries, rows of one vector per lane), as
-// the block-sparse fused kernel runs its CMean (vtx_cmean.h).
+// the block-sparse fused kernel runs its CMean (vtx_cmean.h); its tiles go to
+// the workgroups that finish first, after their own select.
+//
+// The planner's workgroup schedule (sched), the leading preloaded arguments
+// and the check of the predicted bounds (before anything is written) work as
+// in the GQA kernel (indexer_gqa.hip).
 template <int T, int LPR, int VPL, int kG, int kCmRegs>
-__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_fused_kernel(QuestArgs a,
-                                                                                         vtx::CmArgs cma) {
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_fused_kernel(
+    const int32_t* sched, const int64_t* loc, int32_t segments, int32_t loc_n, QuestArgs a, vtx::CmArgs cma) {
   constexpr int kWaves = T / vtx::kWave;
   constexpr int kRowsPerLoad = vtx::kWave / LPR;
   // Two rows per position: half the GeMM's pass keeps the loads of a pass in
@@ -75,7 +82,6 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   __shared__ vtx::SelectShared<T> sh;
   __shared__ vtx::BitonicShared<T> bsh;  // cached segments of up to T pages with k <= 32
 
-  const int seg = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
   const int wave = vtx::uniform(threadIdx.x / vtx::kWave);
@@ -86,16 +92,60 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   const int G = a.G;
 
   long long cm_pos[kLocRegs];
-  if constexpr (cm_on) vtx::closing_load(cma, cm_pos);
-  const long long start = (long long)a.dindptr[seg] + a.bos;
-  const long long n = (long long)a.dindptr[seg + 1] - a.eos - start;
-  const long long obase = (long long)a.sindptr[seg] + a.bos;
-  const bool active = k > 0 && n > k && start >= 0 && start + n <= a.sum_rows && start + n <= a.aggr_len &&
-                      start + n <= a.didx_len && obase >= 0 && obase + k <= a.sidx_len;
+  if constexpr (cm_on) vtx::closing_load(loc, loc_n, cm_pos);
+  const vtx::SchedPick pick = vtx::sched_pick(sched, segments);
+  const int seg = pick.seg;
+  long long start, n, obase;
+  if (pick.predicted) {
+    start = (long long)pick.pe[0] + a.bos;
+    n = (long long)pick.pe[1] - a.eos - start;
+    obase = (long long)pick.pe[2] + a.bos;
+  } else {
+    start = (long long)a.dindptr[seg] + a.bos;
+    n = (long long)a.dindptr[seg + 1] - a.eos - start;
+    obase = (long long)a.sindptr[seg] + a.bos;
+  }
+  auto is_active = [&]() {
+    return k > 0 && n > k && start >= 0 && start + n <= a.sum_rows && start + n <= a.aggr_len &&
+           start + n <= a.didx_len && obase >= 0 && obase + k <= a.sidx_len;
+  };
+  bool active = is_active();
   if constexpr (!cm_on) {
-    if (!active) return;  // uniform: the separate ops write nothing for this segment either
+    if (!active && !pick.predicted) return;  // uniform: the separate ops write nothing for this segment either
+  }
+  // the first pass's row ids, then the check of the predicted bounds, in one
+  // round trip (as in the GQA kernel)
+  long long share = 0;
+  int my_row = -1;
+  auto first_pass = [&]() {
+    share = (n + kWaves - 1) / kWaves;
+    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+    if (share > kPass) share = kPass;
+    const long long p0 = (long long)wave * share;
+    const long long cnt = p0 < n ? min(share, n - p0) : 0;
+    my_row = lane < cnt ? a.didx[start + p0 + lane] : -1;
+  };
+  if (active) first_pass();  // uniform
+  if (pick.predicted) {      // uniform
+    const int32_t* bp = lane == 1 ? a.dindptr + seg + 1 : lane == 2 ? a.sindptr + seg : a.dindptr + seg;
+    const int32_t bv = *bp;
+    const int32_t t0 = __builtin_amdgcn_readlane(bv, 0), t1 = __builtin_amdgcn_readlane(bv, 1),
+                  t2 = __builtin_amdgcn_readlane(bv, 2);
+    if ((t0 != pick.pe[0]) | (t1 != pick.pe[1]) | (t2 != pick.pe[2])) {  // uniform; not for a current schedule
+      start = (long long)t0 + a.bos;
+      n = (long long)t1 - a.eos - start;
+      obase = (long long)t2 + a.bos;
+      active = is_active();
+      if (active) first_pass();
+    }
+  }
+  if constexpr (!cm_on) {
+    if (!active) return;  // uniform
   }
   const bool cached = n <= a.row_cap;
+  // the bitonic select (one key per thread, from LDS) when every page fits
+  // one thread each and k <= 32: no histogram, so no barrier before the rows
+  const bool bitonic = cached && n <= T && k <= vtx::kMaxBitonicK;
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
@@ -103,21 +153,30 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
   const uint16_t* qs = a.q + (long long)seg * G * D;
   vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
-  if (active) {  // uniform
-  vtx::select_init<T>(sel, k, sh);
-  __syncthreads();  // histogram cleared before any wave counts into it
   if constexpr (cm_on) {
     closing = vtx::closing_build(cma, cm_pos);
     n_close = closing.count;
   }
+  // this launch's CMax + CMin: wave w of the workgroup of tile rank r reduces
+  // tiles w * grid + r, ... once its own segment is done
+  auto cm_tiles = [&]() {
+    if constexpr (cm_on)
+      vtx::cmean_tiles<LPR, kLocRegs, vtx::kEnvelope>(cma, closing, wave * (int)gridDim.x + pick.tile_rank,
+                                                      kWaves * (int)gridDim.x, grp, col);
+  };
+  if (!active) {  // uniform (only with the in-launch reduce)
+    cm_tiles();
+    return;
+  }
+  if (!bitonic) {
+    vtx::select_init<T>(sel, k, sh);
+    __syncthreads();  // histogram cleared before any wave counts into it
+  }
 
   // ---- scores, page maxima and keys of every middle page
-  long long share = (n + kWaves - 1) / kWaves;
-  share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
-  if (share > kPass) share = kPass;
   for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
     const int cnt = (int)min(share, n - p0);
-    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
+    if (p0 != (long long)wave * share) my_row = lane < cnt ? dseg[p0 + lane] : -1;  // later passes
     int r = -1;
     float best = -INFINITY;
     for (int g0 = 0; g0 < G; g0 += kG) {
@@ -178,26 +237,18 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
         keys[p0 + r] = (uint16_t)key;
         rows[p0 + r] = my_rid;
       }
-      vtx::select_count<T>(key, sh);
+      if (!bitonic) vtx::select_count<T>(key, sh);
     }
-  }
-  }  // active
-  // this launch's CMax + CMin: wave w of workgroup b reduces tiles w * grid + b, ...
-  if constexpr (cm_on) {
-    if (!active) closing = vtx::closing_build(cma, cm_pos);
-    vtx::cmean_tiles<LPR, kLocRegs, vtx::kEnvelope>(cma, closing, wave * (int)gridDim.x + (int)blockIdx.x,
-                                                    kWaves * (int)gridDim.x, grp, col);
-    if (!active) return;
   }
   __syncthreads();
 
-  // ---- top-k of the segment: the bitonic select (one key per thread, from
-  // LDS) when every page fits one thread each and k <= 32, else the radix
-  // select over the counted keys
-  if (cached && n <= T && k <= vtx::kMaxBitonicK) {  // uniform
+  // ---- top-k of the segment: the bitonic select, else the radix select
+  // over the counted keys
+  if (bitonic) {  // uniform
     const int i = threadIdx.x;
     const uint32_t comp = vtx::bitonic_comp(i < n, i < n ? (uint32_t)keys[i] : 0u, i);
     vtx::select_bitonic<T>(comp, k, bsh, [&](int rk, uint32_t c) { a.sidx[obase + rk] = rows[vtx::bitonic_position(c)]; });
+    cm_tiles();
     return;
   }
   if (cached) {
@@ -207,6 +258,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void quest_
     vtx::select_topk_counted<T>([&](long long i) { return vtx::score_key(ag[i]); }, n, k, sel, sh);
   }
   vtx::select_emit<T>(sel, k, n, [&](int rk, long long pos) { a.sidx[obase + rk] = cached ? rows[pos] : dseg[pos]; });
+  cm_tiles();
 }
 
 constexpr int kLdsBudget = 56 * 1024;  // dynamic LDS; the select tables take up to ~6 KB more
@@ -218,26 +270,43 @@ int launch_dim(const QuestArgs& a, const vtx::CmArgs* cm, int grid, size_t lds, 
   const vtx::CmArgs none{};
   if (cm) {  // the in-kernel CMax + CMin: rows of one 16-byte vector per lane
     const bool one = cm->nnz <= vtx::kWave;
+    const int32_t nnz = (int32_t)cm->nnz;  // at most vtx::kCmLoc
     switch (a.dim) {
       case 64:
-        if (one) quest_fused_kernel<T, 8, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
-        else quest_fused_kernel<T, 8, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        if (one) quest_fused_kernel<T, 8, 1, kG, 1>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
+        else quest_fused_kernel<T, 8, 1, kG, vtx::kCmLoc / vtx::kWave>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
         break;
       case 128:
-        if (one) quest_fused_kernel<T, 16, 1, kG, 1><<<grid, T, lds, s>>>(a, *cm);
-        else quest_fused_kernel<T, 16, 1, kG, vtx::kCmLoc / vtx::kWave><<<grid, T, lds, s>>>(a, *cm);
+        if (one) quest_fused_kernel<T, 16, 1, kG, 1>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
+        else quest_fused_kernel<T, 16, 1, kG, vtx::kCmLoc / vtx::kWave>
+            <<<grid, T, lds, s>>>(a.sched, cm->loc, a.segments, nnz, a, *cm);
         break;
       default: return vtx::fail(VTX_E_INVALID, "indexer_quest_fused: in-kernel page reduce needs head_dim 64 or 128");
     }
     return vtx::check_launch("indexer_quest_fused (with CMax + CMin)");
   }
   switch (a.dim) {
-    case 64: quest_fused_kernel<T, 8, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
-    case 128: quest_fused_kernel<T, 16, 1, kG, 0><<<grid, T, lds, s>>>(a, none); break;
-    case 256: quest_fused_kernel<(T > 512 ? 512 : T), 16, 2, 1, 0><<<grid, (T > 512 ? 512 : T), lds, s>>>(a, none); break;
+    case 64:
+      quest_fused_kernel<T, 8, 1, kG, 0><<<grid, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 128:
+      quest_fused_kernel<T, 16, 1, kG, 0><<<grid, T, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 256:
+      quest_fused_kernel<(T > 512 ? 512 : T), 16, 2, 1, 0>
+          <<<grid, (T > 512 ? 512 : T), lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
     // wide rows keep their query slice in registers: fewer threads, no spills
-    case 512: quest_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1, 0><<<grid, (T > 512 ? 512 : T), lds, s>>>(a, none); break;
-    case 576: quest_fused_kernel<256, 8, 9, 1, 0><<<grid, 256, lds, s>>>(a, none); break;
+    case 512:
+      quest_fused_kernel<(T > 512 ? 512 : T), 16, 4, 1, 0>
+          <<<grid, (T > 512 ? 512 : T), lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
+    case 576:
+      quest_fused_kernel<256, 8, 9, 1, 0><<<grid, 256, lds, s>>>(a.sched, nullptr, a.segments, 0, a, none);
+      break;
     default: return vtx::fail(VTX_E_INVALID, "indexer_quest_fused: head_dim %d not supported", a.dim);
   }
   return vtx::check_launch("indexer_quest_fused");
@@ -271,7 +340,8 @@ int quest_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
                const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
                int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
-               int32_t max_num_pages, const CmeanSpec* cms, void* stream);
+               int32_t max_num_pages, const CmeanSpec* cms, const int32_t* schedule,
+               int64_t schedule_len, void* stream);
 
 }  // namespace
 
@@ -283,12 +353,12 @@ extern "C" int vtx_indexer_quest_fused(const uint16_t* q, int64_t q_rows, int32_
                                        int64_t dense_kv_indices_len, int32_t* sparse_kv_indices,
                                        int64_t sparse_kv_indices_len, int32_t eff_batch_size, int32_t topk_val,
                                        int32_t reserved_bos, int32_t reserved_eos, int32_t max_num_pages,
-                                       void* stream) {
+                                       const int32_t* schedule, int64_t schedule_len, void* stream) {
   vtx::clear_error();
   return quest_impl(q, q_rows, group_size, ymax, ymin, y_rows, head_dim, sum, sum_rows, aggr, aggr_len,
                     dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
                     sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
-                    nullptr, stream);
+                    nullptr, schedule, schedule_len, stream);
 }
 
 extern "C" int vtx_indexer_quest_fused_cmean(const uint16_t* q, int64_t q_rows, int32_t group_size,
@@ -300,7 +370,8 @@ extern "C" int vtx_indexer_quest_fused_cmean(const uint16_t* q, int64_t q_rows, 
                                              int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                                              int32_t reserved_eos, int32_t max_num_pages, const uint16_t* k_cache,
                                              int64_t k_rows, int32_t page_size, int32_t num_kv_heads,
-                                             const int64_t* loc, int64_t nnz, void* stream) {
+                                             const int64_t* loc, int64_t nnz, const int32_t* schedule,
+                                             int64_t schedule_len, void* stream) {
   vtx::clear_error();
   if (!k_cache || (nnz > 0 && !loc))
     return vtx::fail(VTX_E_INVALID, "indexer_quest_fused_cmean: null K pool or loc");
@@ -310,7 +381,7 @@ extern "C" int vtx_indexer_quest_fused_cmean(const uint16_t* q, int64_t q_rows, 
   return quest_impl(q, q_rows, group_size, ymax, ymin, y_rows, head_dim, sum, sum_rows, aggr, aggr_len,
                     dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
                     sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages, &cm,
-                    stream);
+                    schedule, schedule_len, stream);
 }
 
 namespace {
@@ -320,7 +391,8 @@ int quest_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
                const int32_t* dense_kv_indptr, const int32_t* sparse_kv_indptr, const int32_t* dense_kv_indices,
                int64_t dense_kv_indices_len, int32_t* sparse_kv_indices, int64_t sparse_kv_indices_len,
                int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos, int32_t reserved_eos,
-               int32_t max_num_pages, const CmeanSpec* cms, void* stream) {
+               int32_t max_num_pages, const CmeanSpec* cms, const int32_t* schedule,
+               int64_t schedule_len, void* stream) {
   const char* what = "indexer_quest_fused";
   if (eff_batch_size < 0 || reserved_bos < 0 || reserved_eos < 0)
     return vtx::fail(VTX_E_INVALID, "%s: negative size", what);
@@ -370,6 +442,9 @@ int quest_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   a.topk = topk_val > 0 ? topk_val : 0;
   a.bos = reserved_bos;
   a.eos = reserved_eos;
+  // a schedule too short for this launch is not used (the kernel would also
+  // ignore one whose header names another segment count)
+  a.sched = schedule && schedule_len >= vtx::sched_len(1, eff_batch_size) ? schedule : nullptr;
   const long long want = max_num_pages > 0 ? max_num_pages : 0;
   const long long room = (kLdsBudget - (long long)vtx::sel_slots(a.topk) * 8) / 6;  // page id + key per page
   long long cap = want < room ? want : room;

@@ -64,6 +64,42 @@ __device__ __forceinline__ int sched_short_rank32(uint32_t b, uint32_t S, uint32
   return (int)(end - 1u - (b - r * round));
 }
 
+// What workgroup blockIdx.x of a one-workgroup-per-segment launch takes:
+// its segment, whether the schedule names this launch (then pe holds the
+// predicted dense begin, dense end and sparse begin, to be checked against
+// the indptrs before anything is written), and its rank for side work
+// (sched_short_rank32).  Without a schedule (sched null): segment blockIdx.x.
+// The header and the entry are loaded together, and everything after them
+// is branch-free: a load whose value is used only inside a branch is moved
+// into it, and the entry would then wait for the header.
+struct SchedPick {
+  int seg;
+  bool predicted;
+  int32_t pe[3];
+  int tile_rank;
+};
+
+__device__ __forceinline__ SchedPick sched_pick(const int32_t* sched, int32_t segments) {
+  SchedPick p{(int)blockIdx.x, false, {0, 0, 0}, (int)blockIdx.x};
+  if (sched) {  // uniform
+    // workgroups past the segments read the last entry and ignore it
+    const bool mine = (int)blockIdx.x < segments;
+    const int32_t* e = sched + 4 + 4 * (long long)(mine ? blockIdx.x : segments - 1);
+    const int32_t h0 = sched[0], h1 = sched[1], h2 = sched[2];
+    const int32_t e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3];
+    const bool ok = (h0 == kSchedMagic) & (h1 == segments) & (h2 >= 1);
+    p.predicted = mine & ok & (e0 >= 0) & (e0 < segments);
+    p.seg = p.predicted ? e0 : p.seg;
+    p.pe[0] = e1;  // read only when predicted
+    p.pe[1] = e2;
+    p.pe[2] = e3;
+    const int32_t rounds = h2 >= 1 ? h2 : 1;
+    const int rank = sched_short_rank32(blockIdx.x, (uint32_t)segments, (uint32_t)rounds);
+    p.tile_rank = ok ? rank : p.tile_rank;
+  }
+  return p;
+}
+
 __device__ __forceinline__ void sched_write_entry(int32_t* s, long long wg, int32_t seg, int32_t dense_begin,
                                                   int32_t dense_end, int32_t sparse_begin) {
   int32_t* e = s + 4 + 4 * wg;

@@ -73,24 +73,24 @@ _SIGNATURES = {
     ),
     "vtx_indexer_gqa_fused": (
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _i64, _vp],
         ctypes.c_int,
     ),
     "vtx_indexer_gqa_fused_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_indexer_gqa_fused_cmean": (
         [_vp, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _i64, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i64, _vp],
         ctypes.c_int,
     ),
     "vtx_indexer_quest_fused": (
         [_vp, _i64, _i32, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _vp],
+         _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
         ctypes.c_int,
     ),
     "vtx_indexer_quest_fused_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_indexer_quest_fused_cmean": (
         [_vp, _i64, _i32, _vp, _vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
-         _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _vp],
+         _i32, _i32, _i32, _i32, _i32, _vp, _i64, _i32, _i32, _vp, _i64, _vp, _i64, _vp],
         ctypes.c_int,
     ),
     "vtx_ragged_gemm": (
@@ -558,6 +558,14 @@ def indexer_fused_supported(head_dim: int) -> bool:
     return bool(load_library().vtx_indexer_fused_supported(int(head_dim)))
 
 
+def _schedule_args(schedule):
+    """(pointer, length) of a planner-written fused schedule, or (None, 0)."""
+    if schedule is None:
+        return (None, 0)
+    _req(schedule, torch.int32, "schedule")
+    return (schedule.data_ptr(), schedule.numel())
+
+
 @_plain_args
 def indexer_fused(
     q: torch.Tensor,
@@ -640,9 +648,7 @@ def indexer_fused(
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages), D,
             seg_counters.data_ptr() if seg_counters is not None else None,
             seg_counters.numel() if seg_counters is not None else 0, int(mode))
-    if schedule is not None:
-        _req(schedule, torch.int32, "schedule")
-    sched = (schedule.data_ptr() if schedule is not None else None, schedule.numel() if schedule is not None else 0)
+    sched = _schedule_args(schedule)
     if noalloc:
         if seg_counters is not None or cmean is not None:
             raise RuntimeError("vortex_torch: the no-allocation entry point takes no seg_counters and no cmean")
@@ -688,6 +694,7 @@ def indexer_gqa_fused(
     max_num_pages: int,
     softmax_scale=None,
     cmean=None,
+    schedule=None,
 ) -> None:
     """GeMM + segment softmax (unless softmax_scale is None) + max over the
     query heads + topK of one GQA layer in one launch.
@@ -696,10 +703,14 @@ def indexer_gqa_fused(
     buffer [pages, 1, G]; aggr: the Max output buffer [pages, 1, 1]; the
     block tables come from the planner.  cmean: (k_cache [rows, P, D] bf16,
     loc int64, num_kv_heads) — the layer's page-finish mean into y, run first
-    in the same launch (``vtx_indexer_gqa_fused_cmean``).
+    in the same launch (``vtx_indexer_gqa_fused_cmean``).  schedule: the
+    fused_schedule plan_decode wrote for this block table (workgroup order;
+    speed only).
     """
     lib = load_library()
     tensors = [q, y, score, aggr, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
+    if schedule is not None:
+        tensors.append(schedule)
     if cmean is not None:
         tensors += [cmean[0], cmean[1]]
     dev = _require_gpu(*tensors)
@@ -725,6 +736,7 @@ def indexer_gqa_fused(
             sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages),
             0 if softmax_scale is None else 1, float(softmax_scale or 0.0))
+    sched = _schedule_args(schedule)
     if cmean is not None:
         k, loc, heads = cmean
         _req(k, torch.bfloat16, "k_cache")
@@ -733,11 +745,11 @@ def indexer_gqa_fused(
             raise RuntimeError(f"vortex_torch: CMean pool {tuple(k.shape)} does not match head_dim {D}")
         with _on_device(dev):
             rc = lib.vtx_indexer_gqa_fused_cmean(*args, k.data_ptr(), int(k.shape[0]), int(k.shape[1]), int(heads),
-                                                 loc.data_ptr(), loc.numel(), _stream(dev))
+                                                 loc.data_ptr(), loc.numel(), *sched, _stream(dev))
         _check(rc, "indexer_gqa_fused_cmean")
         return
     with _on_device(dev):
-        rc = lib.vtx_indexer_gqa_fused(*args, _stream(dev))
+        rc = lib.vtx_indexer_gqa_fused(*args, *sched, _stream(dev))
     _check(rc, "indexer_gqa_fused")
 
 
@@ -762,6 +774,7 @@ def indexer_quest_fused(
     reserved_eos: int,
     max_num_pages: int,
     envelope=None,
+    schedule=None,
 ) -> None:
     """Quest envelope scores + max over the query heads + topK of one layer
     in one launch.  envelope: (k_cache [rows, P, D] bf16, loc int64,
@@ -770,11 +783,15 @@ def indexer_quest_fused(
 
     q: bf16 [S, G, D]; ymax, ymin: the envelope pools [rows, 1, D]; score:
     the Sum(dim=2) output buffer [pages, G, 1]; aggr: the Max(dim=1) output
-    buffer [pages, 1, 1]; the block tables come from the planner.
+    buffer [pages, 1, 1]; the block tables come from the planner.  schedule:
+    the fused_schedule plan_decode wrote for this block table (workgroup
+    order; speed only).
     """
     lib = load_library()
     tensors = [q, ymax, ymin, score, aggr, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices,
                sparse_kv_indices]
+    if schedule is not None:
+        tensors.append(schedule)
     dev = _require_gpu(*tensors)
     for t, n in ((q, "q"), (ymax, "ymax"), (ymin, "ymin"), (score, "score"), (aggr, "aggr")):
         _req(t, torch.bfloat16, n)
@@ -798,6 +815,7 @@ def indexer_quest_fused(
             dense_kv_indices.data_ptr(), dense_kv_indices.numel(),
             sparse_kv_indices.data_ptr(), sparse_kv_indices.numel(),
             eff, int(topk_val), int(reserved_bos), int(reserved_eos), int(max_num_pages))
+    sched = _schedule_args(schedule)
     if envelope is not None:
         k, loc, heads = envelope
         _require_gpu(k, loc)
@@ -807,11 +825,11 @@ def indexer_quest_fused(
             raise RuntimeError(f"vortex_torch: envelope pool {tuple(k.shape)} does not match head_dim {D}")
         with _on_device(dev):
             rc = lib.vtx_indexer_quest_fused_cmean(*args, k.data_ptr(), int(k.shape[0]), int(k.shape[1]),
-                                                   int(heads), loc.data_ptr(), loc.numel(), _stream(dev))
+                                                   int(heads), loc.data_ptr(), loc.numel(), *sched, _stream(dev))
         _check(rc, "indexer_quest_fused_cmean")
         return
     with _on_device(dev):
-        rc = lib.vtx_indexer_quest_fused(*args, _stream(dev))
+        rc = lib.vtx_indexer_quest_fused(*args, *sched, _stream(dev))
     _check(rc, "indexer_quest_fused")
 
 

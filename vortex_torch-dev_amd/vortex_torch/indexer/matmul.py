@@ -253,7 +253,7 @@ class PendingGemm(_deferred.Pending):
             ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
             ctx.page_reserved_eos, ctx.max_num_pages_per_request,
             softmax_scale=None if self.softmax is None else self.softmax[0],
-            cmean=None if cm is None else (cm.x, cm.loc, cm.ctx.head_num))
+            cmean=None if cm is None else (cm.x, cm.loc, cm.ctx.head_num), schedule=_schedule_of(ctx))
         if cm is not None:
             cm.done = True
         self.done = True

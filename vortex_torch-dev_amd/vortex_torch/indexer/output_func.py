@@ -24,7 +24,7 @@ from .. import _deferred, _hip
 from .._C import topk_output
 from ..abs import FORMAT, vOp, vTensor
 from .context import Context
-from .matmul import PendingGemm, PendingGemv
+from .matmul import PendingGemm, PendingGemv, _schedule_of
 
 
 class topK(vOp):
@@ -123,7 +123,8 @@ def _fuse_quest(chain, o: torch.Tensor, ctx: Context) -> None:
         ctx.dense_kv_indptr, ctx.sparse_kv_indptr, ctx.dense_kv_indices, o,
         ctx.batch_size * ctx.num_kv_heads, ctx.topk_val, ctx.page_reserved_bos,
         ctx.page_reserved_eos, ctx.max_num_pages_per_request,
-        envelope=None if env is None else (env[0].x, env[0].loc, env[0].ctx.head_num))
+        envelope=None if env is None else (env[0].x, env[0].loc, env[0].ctx.head_num),
+        schedule=_schedule_of(ctx))
     if env is not None:
         env[0].done = True
     rsum.done = aggr.done = True
