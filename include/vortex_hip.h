@@ -203,7 +203,11 @@ int vtx_topk_select(const uint16_t* score, int64_t score_len,
  * seg_counters (optional, int32, at least eff_batch_size entries, all zero
  * before the first call) lets the library split long segments over several
  * workgroups: the last workgroup of a segment to finish selects its top-k
- * and sets the segment's counter back to zero.  Calls that share one
+ * and sets the segment's counter back to zero.  With room for
+ * eff_batch_size * 1024 more int32 after the counters (plus one to reach an
+ * 8-byte boundary), each workgroup of a segment split over at most 8 of
+ * them pre-selects its chunk's best k (k <= 64) into that area and the last
+ * one merges the lists; the area needs no initial value.  Calls that share one
  * counter buffer must be ordered on one stream.  mode: VTX_FUSED_AUTO
  * (split when there are fewer than two segments per compute unit and the
  * counters are given), VTX_FUSED_SEGMENT or VTX_FUSED_SPLIT.  Outputs are

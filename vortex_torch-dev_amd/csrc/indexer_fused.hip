@@ -66,7 +66,12 @@ struct FusedArgs {
   int32_t row_cap;   // segments up to this many middle pages are held in LDS
   int32_t segments;  // eff_batch_size; the grid covers all q_rows
   const int32_t* sched;  // the planner's workgroup schedule (vtx_fused_schedule.h), or null
+  // split layout: per segment, kStageLists lists of 64 staged (composite <<
+  // 32 | row id) winners, one per chunk workgroup, or null (no staging)
+  uint64_t* stage;
 };
+
+constexpr int kStageLists = 8;  // staged lists per segment: chunk workgroups that pre-select
 
 constexpr int kMaxQueryDim = 576;  // the widest supported head_dim
 
@@ -512,10 +517,12 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
 
 // Stores / loads performed at device scope (every XCD sees them once the
 // store has completed; no copy in a non-coherent cache is used).
-__device__ __forceinline__ void store_coherent(uint16_t* p, uint16_t v) {
+template <typename V>
+__device__ __forceinline__ void store_coherent(V* p, V v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint16_t load_coherent(const uint16_t* p) {
+template <typename V>
+__device__ __forceinline__ V load_coherent(const V* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -666,6 +673,17 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   }
 
   // ---- scores of this workgroup's chunks
+  // Staged pre-selection: when every workgroup of the segment scores one
+  // chunk, k <= 64 and the lists fit, each workgroup selects its chunk's best
+  // k itself (its row ids by chunk position in LDS) and stages them as one
+  // sorted list, so that the selecting workgroup only merges the lists.  The
+  // composites carry the segment position, unique per page, so the merged
+  // best k are exactly the segment's best k.
+  const bool hier = a.stage != nullptr && k <= vtx::kMaxBitonicRunK && nchunks <= cps && workers <= kWaves &&
+                    kWaves <= kStageLists && n <= a.row_cap && n <= 0xffff;  // uniform
+  int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);  // row ids by position (row_cap entries)
+  uint32_t hcomp = 0;  // hier: this lane's composite and its row id
+  int hrid = 0;
   bool have_mean = mean_in_lds;
   for (long long ch = c; ch < nchunks; ch += cps) {
     const long long c0 = ch * kChunk;
@@ -699,9 +717,24 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
         }
       }
     }
-    if (r >= 0) store_coherent(a.score + start + p0 + r, (uint16_t)vtx::f32_to_bf16(sc));
+    const uint16_t sb = (uint16_t)vtx::f32_to_bf16(sc);
+    if (r >= 0) store_coherent(a.score + start + p0 + r, sb);
+    if (hier) {  // uniform
+      hrid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
+      hcomp = vtx::bitonic_comp(r >= 0, vtx::score_key(sb), (int)(p0 + r));
+    }
   }
   // (wave 0 of chunk 0 always has pages, so the mean has been stored)
+  if (hier && c < workers) {  // uniform: this chunk's best k, staged as list c of the segment
+    const long long c0 = (long long)c * kChunk;
+    if (hcomp) rid_lds[vtx::bitonic_position(hcomp) - c0] = hrid;
+    uint64_t* list = a.stage + ((long long)seg * kStageLists + c) * 64;
+    uint32_t cv[1] = {hcomp};
+    vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {
+      const int32_t rid = cmp ? rid_lds[vtx::bitonic_position(cmp) - c0] : 0;
+      store_coherent(list + rank, ((uint64_t)cmp << 32) | (uint32_t)rid);
+    });
+  }
 
   // ---- arrival: the last of the `workers` workgroups selects.  This is a
   // release/acquire handoff written out for its one kind of payload: the
@@ -732,7 +765,24 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   }
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
-  // ---- top-k of the segment from the stored scores (device-coherent loads)
+  // ---- top-k of the segment
+  if (hier) {  // uniform: merge the staged lists (wave w loads list w; lists past the workers are empty)
+    uint32_t cmp = 0;
+    int32_t rid = 0;
+    if (wave < workers && lane < k) {
+      const uint64_t e = load_coherent(a.stage + ((long long)seg * kStageLists + wave) * 64 + lane);
+      cmp = (uint32_t)(e >> 32);
+      rid = (int32_t)(uint32_t)e;
+    }
+    if (cmp) rid_lds[vtx::bitonic_position(cmp)] = rid;
+    bsr.cand[0][wave * 64 + lane] = cmp;
+    vtx::merge_lists_bitonic_run<T>(k, bsr, [&](int rank, uint32_t cv) {
+      a.sidx[obase + rank] = rid_lds[vtx::bitonic_position(cv)];
+    });
+    cm_tiles();
+    return;
+  }
+  // from the stored scores (device-coherent loads)
   const uint16_t* scs = a.score + start;
   constexpr int kRunR = 4;  // scores per thread of the bitonic select
   if (n <= (long long)T * kRunR && k <= vtx::kMaxBitonicRunK && n <= a.row_cap) {  // uniform
@@ -740,7 +790,6 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
     // workgroup; the sort takes its items in any order, each composite
     // carries its position), past n: position n - 1 again, not an item; the
     // row ids go to LDS by position for the emit
-    int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);
     uint16_t v[kRunR];
     int rid[kRunR];
 #pragma unroll
@@ -1041,6 +1090,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
   a.dim = head_dim;
   a.row_cap = 0;
   a.sched = nullptr;
+  a.stage = nullptr;
 
   if (mode < VTX_FUSED_AUTO || mode > VTX_FUSED_SPLIT)
     return vtx::fail(VTX_E_INVALID, "indexer_fused: unknown mode %d", mode);
@@ -1110,6 +1160,14 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
     if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
     if (items == 0) return VTX_OK;
+    // the staged pre-selection's lists, after the counters (8-byte aligned)
+    // when the workspace holds them: kStageLists * 64 * 2 int32 per segment
+    if (seg_counters) {
+      long long off = eff_batch_size;
+      if (reinterpret_cast<uintptr_t>(seg_counters + off) % 8) ++off;
+      if (seg_counters_len >= off + (long long)eff_batch_size * kStageLists * 128)
+        a.stage = reinterpret_cast<uint64_t*>(seg_counters + off);
+    }
     return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s, cmp);
   }
 
@@ -1204,5 +1262,6 @@ extern "C" int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int3
   return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
                     sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
                     sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
-                    head_dim, counters, kStaticCounters, mode, nullptr, schedule, schedule_len, stream);
+                    head_dim, counters, eff_batch_size, mode, nullptr, schedule, schedule_len,
+                    stream);  // (the counters only: no room for the staged pre-selection)
 }

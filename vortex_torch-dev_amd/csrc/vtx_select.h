@@ -605,9 +605,50 @@ __device__ __forceinline__ void wave_merge_desc2(uint32_t (&v)[2]) {
   bitonic_cx(v[0], v[1], true);
 }
 
+// The k (<= 64) best of the T / 64 lists of 64 composites in bs.cand[0]
+// (list w at w * 64, each sorted descending, 0 for no item), merged pairwise
+// with two elements per lane (element 2l + u; a list against a reversed one
+// is bitonic) until wave 0 holds the best 64 in order: emit(rank, comp) for
+// rank 0 .. k-1, from wave 0.  Every thread of the workgroup calls it; it
+// starts with a barrier (after which bs.cand[0] and whatever else the caller
+// wrote to LDS are visible) and holds one per merge round.
+template <int T, typename Emit>
+__device__ __forceinline__ void merge_lists_bitonic_run(int k, BitonicRunShared<T>& bs, Emit emit) {
+  constexpr int kWaves = T / kWave;
+  static_assert(kWaves >= 2, "two or more lists");
+  const int lane = lane_id();
+  const int wave = uniform(threadIdx.x / kWave);
+  uint32_t v[2] = {0u, 0u};
+  int buf = 0;
+#pragma unroll
+  for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 64 become w / 2
+    __syncthreads();
+    if (wave < w / 2) {  // uniform
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int e = 2 * lane + u;
+        v[u] = e < 64 ? bs.cand[buf][(2 * wave) * 64 + e] : bs.cand[buf][(2 * wave + 1) * 64 + (127 - e)];
+      }
+      wave_merge_desc2(v);
+      if (w > 2 && lane < 32) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) bs.cand[buf ^ 1][wave * 64 + 2 * lane + u] = v[u];
+      }
+    }
+    buf ^= 1;
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (2 * lane + u < k) emit(2 * lane + u, v[u]);
+  }
+}
+
 // The k (<= 64) best of the workgroup's composites, kR per thread (0: none):
-// emit(rank, comp) for rank 0 .. k-1, from wave 0.  Every thread of the
-// workgroup calls it; it contains barriers.
+// each wave sorts its 64 * kR composites descending (strides below kR inside
+// a lane, the others across lanes) and keeps its best 64, then the lists are
+// merged (merge_lists_bitonic_run).  emit(rank, comp) for rank 0 .. k-1,
+// from wave 0.  Every thread of the workgroup calls it; it contains barriers.
 template <int T, int kR, typename Emit>
 __device__ __forceinline__ void select_bitonic_run(uint32_t (&comp)[kR], int k, BitonicRunShared<T>& bs, Emit emit) {
   static_assert(kR >= 1 && (kR & (kR - 1)) == 0 && 64 % kR == 0, "kR: a power of two dividing 64");
@@ -625,30 +666,7 @@ __device__ __forceinline__ void select_bitonic_run(uint32_t (&comp)[kR], int k, 
 #pragma unroll
       for (int u = 0; u < kR; ++u) bs.cand[0][wave * 64 + lane * kR + u] = comp[u];
     }
-    uint32_t v[2] = {0u, 0u};
-    int buf = 0;
-#pragma unroll
-    for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 64 become w / 2
-      __syncthreads();
-      if (wave < w / 2) {  // uniform
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int e = 2 * lane + u;
-          v[u] = e < 64 ? bs.cand[buf][(2 * wave) * 64 + e] : bs.cand[buf][(2 * wave + 1) * 64 + (127 - e)];
-        }
-        wave_merge_desc2(v);
-        if (w > 2 && lane < 32) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u) bs.cand[buf ^ 1][wave * 64 + 2 * lane + u] = v[u];
-        }
-      }
-      buf ^= 1;
-    }
-    if (wave == 0) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-        if (2 * lane + u < k) emit(2 * lane + u, v[u]);
-    }
+    merge_lists_bitonic_run<T>(k, bs, emit);
   }
 }
 

@@ -26,6 +26,9 @@ from ..abs import FORMAT, vOp, vTensor
 from .context import Context
 from .matmul import PendingGemm, PendingGemv, _schedule_of
 
+_STAGE_INT32_PER_SEGMENT = 8 * 64 * 2  # the fused kernel's staged lists (kStageLists of 64 uint64)
+_STAGE_MAX_SEGMENTS = 512              # larger batches take the one-workgroup-per-segment layout
+
 
 class topK(vOp):
     _impl_map: Dict[FORMAT, Callable] = {
@@ -55,7 +58,12 @@ class topK(vOp):
             f"{p}x and o must be on the same device (x.device={x.device}, o.device={o.device})")
         indptr = ctx.dense_kv_indptr
         if isinstance(indptr, torch.Tensor) and indptr.numel() > 1 and x.device.type == "cuda":
-            self.seg_counters = torch.zeros((indptr.numel() - 1,), dtype=torch.int32, device=x.device)
+            # one arrival counter per segment, then (for batches few enough in
+            # segments for the split layout) room for its staged pre-selection:
+            # 8 lists of 64 (composite, row id) pairs per segment
+            S = indptr.numel() - 1
+            stage = S * _STAGE_INT32_PER_SEGMENT + 2 if S <= _STAGE_MAX_SEGMENTS else 0
+            self.seg_counters = torch.zeros((S + stage,), dtype=torch.int32, device=x.device)
 
     def execute(self, x: torch.Tensor, o: torch.Tensor, ctx: Context) -> torch.Tensor:
         assert self.impl is not None, f"{self._prefix()}execute called before profile() (impl is None)"
