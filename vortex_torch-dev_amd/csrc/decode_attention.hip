@@ -166,7 +166,7 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
       for (int g = 0; g < kG; ++g) {
         float s = vtx::dot_row<VPL>(kv[i], qs[g]);
 #pragma unroll
-        for (int d = LPR / 2; d >= 1; d >>= 1) s += __shfl_xor(s, d, vtx::kWave);
+        for (int d = LPR / 2; d >= 1; d >>= 1) s += vtx::xshfl(s, d);
         sc[i][g] = ok[i] ? s * a.scale : -INFINITY;
       }
     // online softmax: the wave's running max covers every token it has seen
@@ -175,7 +175,8 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
       float bm = sc[0][g];
 #pragma unroll
       for (int i = 1; i < kB; ++i) bm = fmaxf(bm, sc[i][g]);
-      for (int d = LPR; d < vtx::kWave; d <<= 1) bm = fmaxf(bm, __shfl_xor(bm, d, vtx::kWave));
+#pragma unroll
+      for (int d = LPR; d < vtx::kWave; d <<= 1) bm = fmaxf(bm, vtx::xshfl(bm, d));
       const float nm = fmaxf(mx[g], bm);
       if (nm == -INFINITY) continue;  // nothing seen yet (wave-uniform)
       const float r = __expf(mx[g] - nm);
@@ -218,12 +219,13 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
   // fold the token groups of the wave (lanes that share col), then the waves
 #pragma unroll
   for (int g = 0; g < kG; ++g) {
+#pragma unroll
     for (int d = LPR; d < vtx::kWave; d <<= 1) {
-      l[g] += __shfl_xor(l[g], d, vtx::kWave);
+      l[g] += vtx::xshfl(l[g], d);
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][v][e] += __shfl_xor(acc[g][v][e], d, vtx::kWave);
+        for (int e = 0; e < 8; ++e) acc[g][v][e] += vtx::xshfl(acc[g][v][e], d);
     }
     if (lane == 0) {
       s_m[wave][g] = mx[g];
