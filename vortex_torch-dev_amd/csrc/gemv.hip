@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kThreads, (VPL == 1 ? 4 : 2)) void gemv_paged_kerne
       }
       // Lanes whose slot is empty or invalid re-read the first valid row of
       // the pass (same cache lines, no extra HBM traffic) and drop the result.
-      int fallback = __shfl(my_row, 0, vtx::kWave);
+      int fallback = __builtin_amdgcn_readlane(my_row, 0);
       if (fallback < 0) fallback = 0;
 
       // Rows are loaded in batches of kBatch slots (all of them when a row is

@@ -34,7 +34,7 @@ __device__ __forceinline__ void row_pass(const uint16_t* const (&ys)[kRows], lon
   constexpr int kBatch = kSlots < kWide ? kSlots : kWide;  // slots loaded together
   static_assert(kSlots >= 1 && kSlots <= LPR && kSlots * kRowsPerLoad == kPass, "pass geometry");
   static_assert(kSlots % kBatch == 0, "batches must tile the slots");
-  int first = __shfl(my_row, 0, kWave);
+  int first = __builtin_amdgcn_readlane(my_row, 0);  // (lane 0's row: a scalar read, no LDS permute)
   if (first < 0 || first >= y_rows) first = 0;
   float acc[kG][kSlots];
 #pragma unroll

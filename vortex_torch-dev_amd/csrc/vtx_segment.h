@@ -82,7 +82,11 @@ __device__ __forceinline__ void column_scan_stats(ValAt val_at, long long cnt, i
     // Power-of-two columns: the lanes of a wave that share a column merge by
     // an xor butterfly (strides cols .. 32), then thread c < cols merges the
     // waves' partials in wave order — two barriers instead of a tree.
-    for (int d = cols; d < kWave; d <<= 1) merge(m, s, __shfl_xor(m, d, kWave), __shfl_xor(s, d, kWave));
+    // (strides cols .. 32 as compile-time constants, so that the shuffles are
+    // VALU ones: d >= cols is uniform)
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1)
+      if (d >= cols) merge(m, s, xshfl(m, d), xshfl(s, d));
     const int wave = tid / kWave;
     if (tid < kScanThreads && (tid % kWave) < cols) {
       pm[wave * cols + c] = m;
