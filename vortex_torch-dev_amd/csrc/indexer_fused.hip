@@ -82,14 +82,15 @@ constexpr int kMaxQueryDim = 576;  // the widest supported head_dim
 // factor inv_g), into qm (LDS row of D bf16) and, when `store`, into x_out
 // row `row`.  Two threads share 16-byte column vector c < D / 8: thread c
 // keeps accumulators 0 and 1, thread D / 8 + c accumulators 2 and 3 and
-// hands them over through `part` (LDS, D / 8 x 16 floats); each loads its 8
+// hands them over through `part` (LDS, D / 8 rows of 16 floats); each loads its 8
 // rows of a round of 16 before adding any, so up to 16 rows take one memory
 // round trip.  Every thread of the workgroup calls it (it holds a barrier);
 // qm is complete after the caller's next barrier.
 constexpr int kMeanRowsIn = 8;  // rows per thread loaded before any is added
+constexpr int kMeanPartStride = 17;  // floats per column in `part`: 16, padded off the LDS banks' period
 
 __device__ __forceinline__ void query_mean_lds(const FusedArgs& a, const uint16_t* qb, int row, bool store,
-                                               uint16_t* qm, float (*part)[16]) {
+                                               uint16_t* qm, float (*part)[kMeanPartStride]) {
   const int D = a.dim;
   const int nv = D / 8;
   for (int base = 0; base < 2 * nv; base += blockDim.x) {  // the same trip count in every thread
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 2)) void indexer_fused_kernel(co
   __shared__ vtx::SelectShared<T> sh;
   __shared__ vtx::BitonicShared<T> bsh;  // kRegSelect with k <= 32: the bitonic select
   __shared__ __align__(16) uint16_t qm_row[VPL * LPR * 8];  // query mean, G > kQRegs
-  __shared__ float qm_part[VPL * LPR][16];                   // its second half's accumulators
+  __shared__ float qm_part[VPL * LPR][kMeanPartStride];      // its second half's accumulators
 
   const int tid = threadIdx.x;
   const int lane = vtx::lane_id();
@@ -571,7 +572,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   __shared__ vtx::BitonicRunShared<T> bsr;  // the selecting workgroup's bitonic select
   __shared__ int s_last;
   __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
-  __shared__ float qm_part[VPL * LPR][16];                                     // its second half's accumulators
+  __shared__ float qm_part[VPL * LPR][kMeanPartStride];                        // its second half's accumulators
   __shared__ __align__(16) uint16_t fresh_row[cm_on && VPL > 1 ? kWaves * kMaxQueryDim : 8];  // per wave, CMean
 
   const int tid = threadIdx.x;
