@@ -13,9 +13,10 @@
 // One workgroup per segment (8 waves, or 4 for wide G x D).  The segment's
 // page rows are staged in LDS first (one load per page, up to kPageCap
 // pages; longer segments read them from the table), so each batch of a
-// wave costs one memory round trip: a wave takes every kWaves-th group of
-// kRowsPerLoad consecutive tokens (LPR lanes per token, 16-byte vectors of K
-// and V), kB groups per batch, and issues the next batch's K and V loads
+// wave costs one memory round trip: a wave takes every kWaves-th batch of
+// kB groups of kRowsPerLoad consecutive tokens (LPR lanes per token, 16-byte
+// vectors of K and V; a batch is one contiguous run of rows), and issues the
+// next batch's K and V loads
 // before it computes on the current one (two register buffers).  It keeps a
 // running max and per-lane partial sums (online softmax); the waves'
 // (max, sum, accumulator) are merged in LDS.  At decode batch sizes the
@@ -128,15 +129,17 @@ __global__ __launch_bounds__((attn_threads<LPR, VPL, kG>()),
   __syncthreads();  // page rows staged
 
   const int groups = (T_tok + kRowsPerLoad - 1) / kRowsPerLoad;
-  // batches of this wave: groups wave + kWaves * (j * kB + i), i < kB
-  const int nb = groups > wave ? (groups - wave + kWaves * kB - 1) / (kWaves * kB) : 0;
+  // batches of this wave: groups (wave + kWaves * j) * kB + i, i < kB (a
+  // batch is kB consecutive groups: one contiguous run of a page's rows)
+  const int batches = (groups + kB - 1) / kB;
+  const int nb = batches > wave ? (batches - wave + kWaves - 1) / kWaves : 0;
 
   // K and V of batch j; tokens past the segment or on rows outside the pool
   // load the pool's first row (a valid address) and are masked off
   auto load = [&](int j, vtx::U4 (&kv)[kB][VPL], vtx::U4 (&vv)[kB][VPL], bool (&ok)[kB]) {
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
-      const int t = (wave + kWaves * (j * kB + i)) * kRowsPerLoad + grp;
+      const int t = ((wave + kWaves * j) * kB + i) * kRowsPerLoad + grp;
       int row = -1, slot = 0;
       if (t < T_tok) {
         const int pg = t / P;
