@@ -66,7 +66,7 @@ HBM_PEAK_GBPS = 8000.0
 # layer's decode CMean.  C2 17,111 KiB fetched + 466 KiB written per launch,
 # C3 17,107 + 464, C5 13,149 + 143, C4 (one pass of CMean + CMax over the
 # closed K tiles) 1,052,803 + 262,144.
-TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_472_685, "c3": 36_026_761, "c5": 27_100_337, "c4": 2_424_391_798}
+TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_498_762, "c3": 36_053_204, "c5": 27_136_366, "c4": 2_424_393_466}
 
 
 def _parse():
