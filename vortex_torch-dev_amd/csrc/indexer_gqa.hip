@@ -135,6 +135,9 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     if (!active) return;  // uniform
   }
   const bool cached = n <= a.row_cap;
+  // the bitonic select (one key per thread, from LDS) when every page fits
+  // one thread each and k <= 32: it needs no histogram
+  const bool bitonic = cached && n <= T && k <= vtx::kMaxBitonicK;  // uniform
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* rows = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(rows + a.row_cap);
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
     cm_tiles();
     return;
   }
-  vtx::select_init<T>(sel, k, sh);
+  if (!bitonic) vtx::select_init<T>(sel, k, sh);
 
   // ---- scores of every middle page for every query head
   for (long long p0 = (long long)wave * share; p0 < n; p0 += (long long)kWaves * share) {
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
       a.aggr[start + i] = (uint16_t)ab;
       const uint32_t key = vtx::score_key(ab);
       if (cached) keys[i] = (uint16_t)key;
-      vtx::select_count<T>(key, sh);
+      if (!bitonic) vtx::select_count<T>(key, sh);
     }
   };
   if (cached) {  // uniform
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : (VPL <= 4 ? 2 : 1))) void gqa_fu
   // ---- top-k of the segment: the bitonic select (one key per thread, from
   // LDS) when every page fits one thread each and k <= 32, else the radix
   // select over the counted keys
-  if (cached && n <= T && k <= vtx::kMaxBitonicK) {  // uniform
+  if (bitonic) {  // uniform
     const int i = threadIdx.x;
     const uint32_t comp = vtx::bitonic_comp(i < n, i < n ? (uint32_t)keys[i] : 0u, i);
     vtx::select_bitonic<T>(comp, k, bsh, [&](int rk, uint32_t c) { a.sidx[obase + rk] = rows[vtx::bitonic_position(c)]; });
