@@ -662,9 +662,12 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* sel_pay = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(sel_pay + k);
-  // the histograms of the final selection are cleared now, off its path (the
-  // barriers of the arrival order this before the counting)
-  vtx::select_init<T>(sel, k, sh);
+  // the histograms of the final selection (the radix selects) are cleared
+  // now, off its path (the barriers of the arrival order this before the
+  // counting); the bitonic selects of the tail use none
+  constexpr int kRunR = 4;  // scores per thread of the tail's bitonic select
+  const bool tail_bitonic = k <= vtx::kMaxBitonicRunK && n <= a.row_cap && n <= (long long)T * kRunR;
+  if (!tail_bitonic) vtx::select_init<T>(sel, k, sh);
   const int32_t* dseg = a.didx + start;
   if (mean_in_lds) {  // workgroup-uniform
     query_mean_lds(a, qb, seg, c == 0, qm_row, qm_part);
@@ -785,8 +788,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   }
   // from the stored scores (device-coherent loads)
   const uint16_t* scs = a.score + start;
-  constexpr int kRunR = 4;  // scores per thread of the bitonic select
-  if (n <= (long long)T * kRunR && k <= vtx::kMaxBitonicRunK && n <= a.row_cap) {  // uniform
+  if (tail_bitonic) {  // uniform
     // thread t holds positions u * T + t (each load coalesced across the
     // workgroup; the sort takes its items in any order, each composite
     // carries its position), past n: position n - 1 again, not an item; the
