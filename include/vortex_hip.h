@@ -200,15 +200,18 @@ int vtx_topk_select(const uint16_t* score, int64_t score_len,
  * With group_size == 0 the query rows are taken from x [S, D] instead.
  * q: bf16 [q_rows, group_size, head_dim]; y: bf16 [y_rows, head_dim].
  *
- * seg_counters (optional, int32, at least eff_batch_size entries, all zero
- * before the first call) lets the library split long segments over several
- * workgroups: the last workgroup of a segment to finish selects its top-k
- * and sets the segment's counter back to zero.  With room for
- * eff_batch_size * 1024 more int32 after the counters (plus one to reach an
- * 8-byte boundary), each workgroup of a segment split over at most 8 of
- * them pre-selects its chunk's best k (k <= 64) into that area and the last
- * one merges the lists; the area needs no initial value.  Calls that share one
- * counter buffer must be ordered on one stream.  mode: VTX_FUSED_AUTO
+ * seg_counters (optional, int32, seg_counters_len entries) is the split
+ * layout's workspace: it lets the library split long segments over several
+ * workgroups.  Its first entries are per-segment arrival counters, all zero
+ * before the first call: the last workgroup of a segment to finish selects
+ * its top-k and sets the segment's counter back to zero.  A workspace of
+ * vtx_indexer_fused_workspace_len(S) entries serves every call with up to
+ * S segments: it also holds, at its end, the staging zone in which each
+ * workgroup of a segment split over at most 16 of them pre-selects its
+ * chunk's best k (k <= 64), so that the last one only merges the lists; the
+ * zone needs no initial value, and the counters are the entries before it.
+ * A shorter buffer (at least eff_batch_size entries) holds counters only.
+ * Calls that share one workspace must be ordered on one stream.  mode: VTX_FUSED_AUTO
  * (split when there are fewer than two segments per compute unit and the
  * counters are given), VTX_FUSED_SEGMENT or VTX_FUSED_SPLIT.  Outputs are
  * identical in every mode.
@@ -230,16 +233,27 @@ int vtx_indexer_fused(const uint16_t* q, int64_t q_rows, int32_t group_size,
                       const int32_t* schedule, int64_t schedule_len, void* stream);
 
 /*
+ * Entries (int32) of a vtx_indexer_fused workspace that serves calls with up
+ * to `segments` segments, staged pre-selection included; -1 for a negative
+ * count.  Allocate it zeroed once and pass it to every call.
+ */
+int64_t vtx_indexer_fused_workspace_len(int32_t segments);
+
+/*
  * vtx_indexer_fused without the seg_counters workspace: the split layout's
- * per-segment arrival counters live in a device array of the library
- * (65,536 int32 per device, held until the process ends), so the call
- * allocates nothing and takes no workspace.  No counterpart in the
+ * workspace (65,536 arrival counters and the staging zone, 4.25 MiB per
+ * device, held until the process ends) is a device array of the library, so
+ * the call allocates nothing and takes no workspace.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under graph
  * capture, tight serving loops, harnesses that forbid allocation).  The
- * first call on a device looks the array up and clears it (a fill kernel on
- * `stream`).  At most 65,536 segments (eff_batch_size), else VTX_E_INVALID.
- * Every call on a device shares the array: calls that overlap on one device
- * (other streams, other threads) race and must be serialized by the caller.
+ * first call on a device looks the array up and clears its counters (a fill
+ * kernel on `stream`, waited for unless the stream is being captured).  At
+ * most 65,536 segments (eff_batch_size), else VTX_E_INVALID.  Every call on
+ * a device shares the array: calls that overlap on one device (other
+ * streams, other threads) race and must be serialized by the caller.  A
+ * launch that fails (VTX_E_LAUNCH) has the counters cleared again before the
+ * next call; after a launch that was issued but did not complete (an aborted
+ * stream), call vtx_indexer_fused_noalloc_reset.
  */
 int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int32_t group_size,
                               const uint16_t* x, uint16_t* x_out, const uint16_t* y,
@@ -250,6 +264,13 @@ int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int32_t group_s
                               int32_t eff_batch_size, int32_t topk_val, int32_t reserved_bos,
                               int32_t reserved_eos, int32_t max_num_pages, int32_t head_dim,
                               int32_t mode, const int32_t* schedule, int64_t schedule_len, void* stream);
+
+/*
+ * Clears the arrival counters of vtx_indexer_fused_noalloc's workspace on the
+ * current device (a fill kernel on `stream`, waited for unless the stream is
+ * being captured).  Allocates nothing.  No counterpart in the reference.
+ */
+int vtx_indexer_fused_noalloc_reset(void* stream);
 
 /* 1 if vtx_indexer_fused handles this head_dim (64, 128, 256, 512, 576). */
 int vtx_indexer_fused_supported(int32_t head_dim);
@@ -613,6 +634,26 @@ int vtx_paged_decode_attention(const uint16_t* q, uint16_t* o, const uint16_t* k
 
 /* 1 if vtx_paged_decode_attention handles this head_dim and group size. */
 int vtx_paged_decode_attention_supported(int32_t head_dim, int32_t group_size);
+
+/*
+ * Bandwidth probes (measurement only; no counterpart in the reference).
+ * vtx_probe_read reads `bytes` of src sequentially (16-byte nontemporal
+ * loads, grid-stride over four 512-thread workgroups per compute unit).
+ * vtx_probe_gather reads rows rows[0 .. n_rows) of pool ([pool_rows,
+ * row_bytes] bytes, row_bytes 256 or 1152) in the indexer's scoring passes
+ * (per wave one coalesced load of 64 or 16 row ids, then every row load of
+ * the pass in flight); with indptr (segments entries) each workgroup first
+ * loads one indptr entry and only then its row ids, the fused kernel's chain
+ * of dependent trips.  Neither writes anything unless a lane's fold of the
+ * loaded words equals `magic` (sink: one uint32 per thread, at least 2048 per
+ * compute unit for the read and one per row id rounded up to 512 for the
+ * gather).
+ */
+int vtx_probe_read(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_len, uint32_t magic,
+                   void* stream);
+int vtx_probe_gather(const uint16_t* pool, int64_t pool_rows, int32_t row_bytes, const int32_t* rows,
+                     int64_t n_rows, const int32_t* indptr, int32_t segments, uint32_t* sink,
+                     int64_t sink_len, uint32_t magic, void* stream);
 
 #ifdef __cplusplus
 }

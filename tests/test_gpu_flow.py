@@ -468,8 +468,14 @@ def test_flow_cmean_carried_into_indexer_launch(gpu, name, monkeypatch):
     np.testing.assert_array_equal(results["1"][2][cov], results["0"][2][cov])
 
 
+def _c5_top64():
+    b = W.c5()
+    b.topk = 64  # 16 staged lists of 64: four entries per thread in the merge
+    return b
+
+
 @pytest.mark.parametrize("kind", ["random", "ties", "const"])
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "r0", "r3", "r5", "r9"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "c5k64", "r0", "r3", "r5", "r9"])
 def test_split_staged_preselect_equals_unstaged(gpu, name, kind):
     """The split layout with room for the staged pre-selection after the
     counters (every chunk workgroup stages its chunk's best k, the last one
@@ -479,7 +485,7 @@ def test_split_staged_preselect_equals_unstaged(gpu, name, kind):
     the selection is the oracle's stable order."""
     dev = gpu
     batch = {"r0": lambda: W.random_small(0), "r3": lambda: W.random_small(3), "r5": lambda: W.random_small(5),
-             "r9": lambda: W.random_small(9)}.get(name, getattr(W, name, None))()
+             "r9": lambda: W.random_small(9), "c5k64": _c5_top64}.get(name, getattr(W, name, None))()
     ic, _ = W.make_contexts(batch, dev)
     _plan(batch, ic, dev)
     H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
@@ -496,7 +502,7 @@ def test_split_staged_preselect_equals_unstaged(gpu, name, kind):
     qin = q if G <= 16 else q.mean(dim=1, keepdim=True)
     out = {}
     for staged in (False, True):
-        counters = torch.zeros(S + (S * 1024 + 2 if staged else 0), dtype=torch.int32, device=dev)
+        counters = torch.zeros(_hip.indexer_fused_workspace_len(S) if staged else S, dtype=torch.int32, device=dev)
         for _ in range(2):
             qm = torch.full((S, 1, D), 3.0, device=dev, dtype=torch.bfloat16)
             sc = torch.full((ic.dense_kv_indices.numel(), 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
@@ -513,3 +519,55 @@ def test_split_staged_preselect_equals_unstaged(gpu, name, kind):
         exp, _ = O.topk(out[True][1], _np(ic.dense_kv_indptr), _np(ic.sparse_kv_indptr),
                         _np(ic.dense_kv_indices), _np(ic.sparse_kv_indices), S, batch.topk, batch.bos, batch.eos)
         np.testing.assert_array_equal(out[True][2], exp)
+
+
+def _split_case(batch, dev, seed):
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    H, G, D = batch.num_kv_heads, batch.group_size, batch.head_dim
+    S = batch.batch * H
+    q = W.randn_bf16((S, G, D), seed, dev)
+    y = W.randn_bf16((batch.pool_pages * H, 1, D), seed + 1, dev, std=0.25)
+    return ic, q, y, S
+
+
+def _split_run(batch, case, workspace):
+    ic, q, y, S = case
+    D = batch.head_dim
+    qm = torch.full((S, 1, D), 3.0, device=q.device, dtype=torch.bfloat16)
+    sc = torch.full((ic.dense_kv_indices.numel(), 1, 1), -5.0, device=q.device, dtype=torch.bfloat16)
+    sp = ic.sparse_kv_indices.clone()
+    _hip.indexer_fused(q, qm, y, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp, S,
+                       batch.topk, batch.bos, batch.eos, batch.max_pages_per_request, seg_counters=workspace,
+                       mode=_hip.FUSED_SPLIT)
+    torch.cuda.synchronize()
+    return _bits(qm), _bits(sc), _np(sp)
+
+
+def test_split_workspace_shared_by_batches_of_several_sizes(gpu):
+    """One workspace serves a decode loop whose segment count changes from
+    call to call (growing and shrinking, as SGLang's batches do): every call
+    equals the same call on a fresh zeroed workspace and on a counters-only
+    buffer (the unstaged path), bit for bit, and leaves every counter the
+    workspace holds at zero."""
+    dev = gpu
+    cap = 512
+    ws = torch.zeros(_hip.indexer_fused_workspace_len(cap), dtype=torch.int32, device=dev)
+    small = W.make_batch([3000, 9000, 700], pool_pages=900, seed=51, num_kv_heads=2, group_size=2,
+                         head_dim=128, topk=20, bos=1, eos=1)
+    mid = W.make_batch([2500 + 97 * i for i in range(40)], pool_pages=12000, seed=52, num_kv_heads=8,
+                       group_size=2, head_dim=128, topk=30, bos=1, eos=1)
+    wide = W.make_batch([5000, 7000, 9000], pool_pages=2000, seed=53, num_kv_heads=1, group_size=16,
+                        head_dim=576, topk=32, bos=1, eos=1)
+    seq = [(W.c3(), 5), (small, 6), (W.c3(), 5), (mid, 7), (wide, 8), (small, 6), (mid, 7)]
+    for i, (batch, seed) in enumerate(seq):
+        case = _split_case(batch, dev, seed)
+        S = case[3]
+        assert S <= cap
+        got = _split_run(batch, case, ws)
+        assert int(ws[:cap].abs().sum()) == 0, f"call {i}: counters not back at zero"
+        fresh = _split_run(batch, case, torch.zeros_like(ws))
+        plain = _split_run(batch, case, torch.zeros(S, dtype=torch.int32, device=dev))
+        for a, b, c in zip(got, fresh, plain):
+            np.testing.assert_array_equal(a, b)
+            np.testing.assert_array_equal(a, c)

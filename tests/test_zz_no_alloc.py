@@ -1,12 +1,14 @@
 """GPU test of vtx_indexer_fused_noalloc, the entry point that allocates
-nothing: the split layout's per-segment arrival counters live in a device
-array of the library instead of a caller workspace.
+nothing: the split layout's workspace (per-segment arrival counters and the
+staging zone of its pre-selection) lives in a device array of the library
+instead of a caller workspace.
 
 Through the C-ABI (ctypes), two calls in a row — a layout of 64 segments
 split over many workgroups, then a smaller one — each compared bit for bit
-with vtx_indexer_fused given a zeroed workspace: q-mean, scores and block
-table.  A third call repeats the first layout, which only gives the same
-result if the earlier calls left every counter at zero.
+with vtx_indexer_fused given zeroed counters only (so also the staged
+pre-selection against the unstaged path): q-mean, scores and block table.
+A third call repeats the first layout, which only gives the same result if
+the earlier calls left every counter at zero.
 """
 import numpy as np
 import pytest
@@ -58,6 +60,21 @@ def test_noalloc_entry_point_equals_workspace_entry_point(gpu, mode):
         ic, q, y, S = _case(batch, gpu, seed)
         got = _run(batch, ic, q, y, S, mode, noalloc=True)
         exp = _run(batch, ic, q, y, S, mode, noalloc=False)
+        for a, b in zip(got, exp):
+            np.testing.assert_array_equal(a, b)
+
+
+def test_noalloc_reset_then_calls_equal_workspace_entry_point(gpu):
+    """vtx_indexer_fused_noalloc_reset clears the library's counters; calls
+    after it (a larger batch after a smaller one) still equal the workspace
+    entry point bit for bit."""
+    _hip.indexer_fused_noalloc_reset(gpu)
+    small = (W.make_batch([3000, 9000, 700], pool_pages=900, seed=51, num_kv_heads=2, group_size=2,
+                          head_dim=128, topk=20, bos=1, eos=1), 2)
+    for batch, seed in (small, (W.c3(), 1)):
+        ic, q, y, S = _case(batch, gpu, seed)
+        got = _run(batch, ic, q, y, S, _hip.FUSED_SPLIT, noalloc=True)
+        exp = _run(batch, ic, q, y, S, _hip.FUSED_SPLIT, noalloc=False)
         for a, b in zip(got, exp):
             np.testing.assert_array_equal(a, b)
 

@@ -66,12 +66,23 @@ struct FusedArgs {
   int32_t row_cap;   // segments up to this many middle pages are held in LDS
   int32_t segments;  // eff_batch_size; the grid covers all q_rows
   const int32_t* sched;  // the planner's workgroup schedule (vtx_fused_schedule.h), or null
-  // split layout: per segment, kStageLists lists of 64 staged (composite <<
-  // 32 | row id) winners, one per chunk workgroup, or null (no staging)
+  // split layout: per segment, kStageLists lists of kStageListLen staged
+  // (composite << 32 | row id) winners, one per chunk workgroup, or null (no
+  // staging)
   uint64_t* stage;
 };
 
-constexpr int kStageLists = 8;  // staged lists per segment: chunk workgroups that pre-select
+// The staging zone of the split layout's pre-selection: kStageLists lists
+// of kStageListLen entries for each of up to kStageMaxSegments segments, at
+// the end of the caller's workspace (kStageZoneInts int32, two of them
+// slack for the 8-byte alignment).  Its place depends only on the
+// workspace's length, so no call's counters (at the workspace's start, at
+// most length - kStageZoneInts of them) ever overlap lists an earlier call
+// staged, whatever the segment counts of the two calls.
+constexpr int kStageLists = 16;        // staged lists per segment: chunk workgroups that pre-select
+constexpr int kStageListLen = 64;      // entries per list (k <= 64)
+constexpr int kStageMaxSegments = 512;  // segments of a call that stages (the split layout's range)
+constexpr long long kStageZoneInts = (long long)kStageMaxSegments * kStageLists * kStageListLen * 2 + 2;
 
 constexpr int kMaxQueryDim = 576;  // the widest supported head_dim
 
@@ -530,6 +541,41 @@ __device__ __forceinline__ V load_coherent(const V* p) {
 // Histogram copies of the split layout's selection (vtx::SelectShared).
 constexpr int kSplitHistCopies = 8;
 
+// The split layout's final select over the staged lists at `lists` (list j
+// at j * kStageListLen: the best cnt_j = min(k, pages of chunk j) of chunk
+// j, descending, composites in the high half, row ids in the low half): the
+// k best of the workers lists, emit(rank, composite) for rank 0 .. k-1 (from
+// wave 0); each row id goes to rid_lds at its composite's segment position.
+// Lane l of wave w holds the elements g = (w * 64 + l) * kR + u, element g
+// being place g % lk of list g / lk (lk = k rounded up to a power of two, so
+// the lists are sorted runs of lk elements), every other list reversed when
+// a wave holds several, so that the bitonic sort starts at runs of 2 * lk.
+// Every thread of the workgroup calls it (it holds barriers).
+template <int T, int kR, typename Emit>
+__device__ __forceinline__ void merge_staged(const uint64_t* lists, int workers, int k, int lk, long long n,
+                                             int chunk, int32_t* rid_lds, vtx::BitonicRunShared<T>& bs, Emit emit) {
+  const int lane = vtx::lane_id();
+  const int wave = vtx::uniform(threadIdx.x / vtx::kWave);
+  const bool alternate = vtx::kWave * kR >= 2 * lk;
+  uint64_t e[kR];
+  bool ok[kR];
+#pragma unroll
+  for (int u = 0; u < kR; ++u) {  // every load issued before any is used (list 0, place 0 always exists)
+    const int g = (wave * vtx::kWave + lane) * kR + u;
+    const int list = g / lk, p = g % lk;
+    const int place = (alternate && (list & 1)) ? lk - 1 - p : p;
+    ok[u] = list < workers && place < k && place < n - (long long)list * chunk;
+    e[u] = load_coherent(lists + (ok[u] ? (long long)list * kStageListLen + place : 0));
+  }
+  uint32_t comp[kR];
+#pragma unroll
+  for (int u = 0; u < kR; ++u) {
+    comp[u] = ok[u] ? (uint32_t)(e[u] >> 32) : 0u;
+    if (comp[u]) rid_lds[vtx::bitonic_position(comp[u])] = (int32_t)(uint32_t)e[u];
+  }
+  vtx::select_bitonic_run<T, kR>(comp, k, bs, emit, alternate ? lk : vtx::kWave * kR);
+}
+
 // Split segments: a segment's middle pages are dealt, kChunk = kWaves * kPass
 // at a time, to `cps` workgroups (chunk c takes chunks c, c + cps, ...).  Each
 // workgroup scores its pages and stores the scores; the one that finishes
@@ -678,13 +724,16 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
 
   // ---- scores of this workgroup's chunks
   // Staged pre-selection: when every workgroup of the segment scores one
-  // chunk, k <= 64 and the lists fit, each workgroup selects its chunk's best
-  // k itself (its row ids by chunk position in LDS) and stages them as one
-  // sorted list, so that the selecting workgroup only merges the lists.  The
-  // composites carry the segment position, unique per page, so the merged
-  // best k are exactly the segment's best k.
-  const bool hier = a.stage != nullptr && k <= vtx::kMaxBitonicRunK && nchunks <= cps && workers <= kWaves &&
-                    kWaves <= kStageLists && n <= a.row_cap && n <= 0xffff;  // uniform
+  // chunk, k <= 64 and the segment has at most kStageLists chunks, each
+  // workgroup selects its chunk's best k itself (its row ids by chunk
+  // position in LDS) and stages them as one sorted list, so that the
+  // selecting workgroup only merges the lists.  The composites carry the
+  // segment position, unique per page, so the merged best k are exactly the
+  // segment's best k.  The selecting workgroup then reads only the lists:
+  // the scores are stored with ordinary stores (visible when the launch
+  // ends), only the lists are written through for the hand-off.
+  const bool hier = a.stage != nullptr && seg < kStageMaxSegments && k <= vtx::kMaxBitonicRunK &&
+                    nchunks <= cps && workers <= kStageLists && n <= a.row_cap && n <= 0xffff;  // uniform
   int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);  // row ids by position (row_cap entries)
   uint32_t hcomp = 0;  // hier: this lane's composite and its row id
   int hrid = 0;
@@ -722,7 +771,10 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
       }
     }
     const uint16_t sb = (uint16_t)vtx::f32_to_bf16(sc);
-    if (r >= 0) store_coherent(a.score + start + p0 + r, sb);
+    if (r >= 0) {
+      if (hier) a.score[start + p0 + r] = sb;  // read by no other workgroup of the launch
+      else store_coherent(a.score + start + p0 + r, sb);
+    }
     if (hier) {  // uniform
       hrid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
       hcomp = vtx::bitonic_comp(r >= 0, vtx::score_key(sb), (int)(p0 + r));
@@ -732,11 +784,10 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   if (hier && c < workers) {  // uniform: this chunk's best k, staged as list c of the segment
     const long long c0 = (long long)c * kChunk;
     if (hcomp) rid_lds[vtx::bitonic_position(hcomp) - c0] = hrid;
-    uint64_t* list = a.stage + ((long long)seg * kStageLists + c) * 64;
+    uint64_t* list = a.stage + ((long long)seg * kStageLists + c) * kStageListLen;
     uint32_t cv[1] = {hcomp};
     vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {
-      const int32_t rid = cmp ? rid_lds[vtx::bitonic_position(cmp) - c0] : 0;
-      store_coherent(list + rank, ((uint64_t)cmp << 32) | (uint32_t)rid);
+      if (cmp) store_coherent(list + rank, ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0]);
     });
   }
 
@@ -770,19 +821,24 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   // ---- top-k of the segment
-  if (hier) {  // uniform: merge the staged lists (wave w loads list w; lists past the workers are empty)
-    uint32_t cmp = 0;
-    int32_t rid = 0;
-    if (wave < workers && lane < k) {
-      const uint64_t e = load_coherent(a.stage + ((long long)seg * kStageLists + wave) * 64 + lane);
-      cmp = (uint32_t)(e >> 32);
-      rid = (int32_t)(uint32_t)e;
+  if (hier) {  // uniform: merge the staged lists
+    // entries: workers lists of lk = k rounded up to a power of two places,
+    // kR per thread
+    const int lk = k <= 1 ? 1 : 1 << (32 - __builtin_clz((unsigned)(k - 1)));
+    const int total = workers * lk;
+    auto merge = [&](auto kr_tag) {
+      constexpr int kR = decltype(kr_tag)::value;
+      merge_staged<T, kR>(a.stage + (long long)seg * kStageLists * kStageListLen, workers, k, lk, n, kChunk, rid_lds,
+                          bsr, [&](int rank, uint32_t cv) { a.sidx[obase + rank] = rid_lds[vtx::bitonic_position(cv)]; });
+    };
+    if (total <= T) {
+      merge(std::integral_constant<int, 1>{});
+    } else if constexpr (T >= 512) {  // (total <= kStageLists * kStageListLen = 2 * 512)
+      merge(std::integral_constant<int, 2>{});
+    } else {
+      if (total <= 2 * T) merge(std::integral_constant<int, 2>{});
+      else merge(std::integral_constant<int, 4>{});
     }
-    if (cmp) rid_lds[vtx::bitonic_position(cmp)] = rid;
-    bsr.cand[0][wave * 64 + lane] = cmp;
-    vtx::merge_lists_bitonic_run<T>(k, bsr, [&](int rank, uint32_t cv) {
-      a.sidx[obase + rank] = rid_lds[vtx::bitonic_position(cv)];
-    });
     cm_tiles();
     return;
   }
@@ -981,6 +1037,10 @@ extern "C" int vtx_indexer_fused_supported(int32_t head_dim) {
   return head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512 || head_dim == 576;
 }
 
+extern "C" int64_t vtx_indexer_fused_workspace_len(int32_t segments) {
+  return segments < 0 ? -1 : (int64_t)segments + kStageZoneInts;
+}
+
 namespace {
 
 // The decode CMean a fused launch may run first (vtx_indexer_fused_cmean).
@@ -1097,10 +1157,21 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
 
   if (mode < VTX_FUSED_AUTO || mode > VTX_FUSED_SPLIT)
     return vtx::fail(VTX_E_INVALID, "indexer_fused: unknown mode %d", mode);
-  const bool have_counters = seg_counters && seg_counters_len >= eff_batch_size;
+  // The workspace: the arrival counters at its start; when it is at least
+  // kStageZoneInts long, the staging zone at its end, and the counters are
+  // the int32s before the zone (so none of them ever holds a staged list)
+  long long counter_cap = seg_counters ? seg_counters_len : 0;
+  uint64_t* zone = nullptr;
+  if (seg_counters && seg_counters_len >= kStageZoneInts) {
+    counter_cap = seg_counters_len - kStageZoneInts;
+    long long off = counter_cap;
+    if (reinterpret_cast<uintptr_t>(seg_counters + off) % 8) ++off;
+    zone = reinterpret_cast<uint64_t*>(seg_counters + off);
+  }
+  const bool have_counters = seg_counters && counter_cap >= eff_batch_size;
   if (mode == VTX_FUSED_SPLIT && !have_counters)
     return vtx::fail(VTX_E_INVALID, "indexer_fused: split mode needs %d segment counters, got %lld",
-                     eff_batch_size, (long long)(seg_counters ? seg_counters_len : 0));
+                     eff_batch_size, counter_cap);
   a.segments = eff_batch_size;
   const long long want = max_num_pages > 0 ? max_num_pages : 0;
   hipStream_t s = vtx::as_stream(stream);
@@ -1131,6 +1202,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     cma.nnz = cms->nnz;
     cma.heads = cms->heads;
     cma.page = cms->page_size;
+    cma.page_shift = vtx::log2_exact(cms->page_size);
   }
   const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
   if (cms && !cm_inside && cms->nnz > 0) {
@@ -1163,14 +1235,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
     if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
     if (items == 0) return VTX_OK;
-    // the staged pre-selection's lists, after the counters (8-byte aligned)
-    // when the workspace holds them: kStageLists * 64 * 2 int32 per segment
-    if (seg_counters) {
-      long long off = eff_batch_size;
-      if (reinterpret_cast<uintptr_t>(seg_counters + off) % 8) ++off;
-      if (seg_counters_len >= off + (long long)eff_batch_size * kStageLists * 128)
-        a.stage = reinterpret_cast<uint64_t*>(seg_counters + off);
-    }
+    a.stage = zone;  // the staged pre-selection's lists (segments past kStageMaxSegments do not stage)
     return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s, cmp);
   }
 
@@ -1198,20 +1263,24 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// vtx_indexer_fused_noalloc: vtx_indexer_fused with the split layout's
-// per-segment arrival counters in a file-scope device array instead of a
-// caller workspace, for callers that cannot allocate.  Every device keeps its
-// own copy of the array until the process ends; the kernels take its device
-// address (queried once per device with that device current), never the
-// host-side name.  Each launch leaves every counter it used at zero, so the
-// array only needs clearing once, by a fill kernel on the first call's
-// stream.  Calls that overlap on one device share the counters and race.
+// vtx_indexer_fused_noalloc: vtx_indexer_fused with its workspace (the split
+// layout's per-segment arrival counters and the staging zone of its
+// pre-selection) in a file-scope device array instead of a caller buffer,
+// for callers that cannot allocate.  Every device keeps its own copy of the
+// array until the process ends; the kernels take its device address
+// (queried once per device with that device current), never the host-side
+// name.  Each launch that completes leaves every counter it used at zero, so
+// the counters are cleared (by a fill kernel) on the first call on a device,
+// by vtx_indexer_fused_noalloc_reset, and again before the next call after a
+// launch this entry point could not issue.  Calls that overlap on one device
+// share the array and race.
 #include <mutex>
 
 namespace {
 
 constexpr int64_t kStaticCounters = 65536;  // segments a no-allocation call may have
-static __device__ __align__(256) int32_t scratch[kStaticCounters];
+constexpr int64_t kStaticInts = kStaticCounters + kStageZoneInts;  // 4.25 MiB
+static __device__ __align__(256) int32_t scratch[kStaticInts];
 
 __global__ void clear_counters_kernel(int32_t* c, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -1221,9 +1290,25 @@ __global__ void clear_counters_kernel(int32_t* c, int64_t n) {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 int32_t* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+bool g_scratch_dirty[kMaxDevices] = {};    // counters to clear before the next call
 
-// This device's counters (set up on the first call on the device).
-int static_counters(hipStream_t s, int32_t** out) {
+// Clears the counters on stream s; outside a graph capture it also waits for
+// the fill, so that a first call on another stream cannot run before it.
+int clear_counters(int32_t* p, hipStream_t s) {
+  clear_counters_kernel<<<64, 256, 0, s>>>(p, kStaticCounters);
+  int rc = vtx::check_launch("indexer_fused_noalloc (clearing the counters)");
+  if (rc != VTX_OK) return rc;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess)
+    return vtx::fail(VTX_E_DEVICE, "indexer_fused_noalloc: cannot query the stream's capture state");
+  if (st == hipStreamCaptureStatusNone && hipStreamSynchronize(s) != hipSuccess)
+    return vtx::fail(VTX_E_DEVICE, "indexer_fused_noalloc: clearing the counters failed");
+  return VTX_OK;
+}
+
+// This device's workspace, set up (address looked up, counters cleared) on
+// the first call on the device and cleared again when marked dirty.
+int static_counters(hipStream_t s, bool force_clear, int32_t** out, int* dev_out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return vtx::fail(VTX_E_DEVICE, "indexer_fused_noalloc: no usable current device");
@@ -1234,12 +1319,16 @@ int static_counters(hipStream_t s, int32_t** out) {
     if (e != hipSuccess || !p)
       return vtx::fail(VTX_E_DEVICE, "indexer_fused_noalloc: cannot get the counters' address: %s",
                        hipGetErrorString(e));
-    clear_counters_kernel<<<64, 256, 0, s>>>(static_cast<int32_t*>(p), kStaticCounters);
-    const int rc = vtx::check_launch("indexer_fused_noalloc (clearing the counters)");
-    if (rc != VTX_OK) return rc;
     g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+    g_scratch_dirty[dev] = true;
+  }
+  if (g_scratch_dirty[dev] || force_clear) {
+    const int rc = clear_counters(g_scratch_ptr[dev], s);
+    if (rc != VTX_OK) return rc;
+    g_scratch_dirty[dev] = false;
   }
   *out = g_scratch_ptr[dev];
+  *dev_out = dev;
   return VTX_OK;
 }
 
@@ -1260,11 +1349,23 @@ extern "C" int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int3
     return vtx::fail(VTX_E_INVALID, "indexer_fused_noalloc: %d segments exceed the %lld it serves",
                      eff_batch_size, (long long)kStaticCounters);
   int32_t* counters = nullptr;
-  const int rc = static_counters(vtx::as_stream(stream), &counters);
+  int dev = -1;
+  int rc = static_counters(vtx::as_stream(stream), false, &counters, &dev);
   if (rc != VTX_OK) return rc;
-  return fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr,
-                    sparse_kv_indptr, dense_kv_indices, dense_kv_indices_len, sparse_kv_indices,
-                    sparse_kv_indices_len, eff_batch_size, topk_val, reserved_bos, reserved_eos, max_num_pages,
-                    head_dim, counters, eff_batch_size, mode, nullptr, schedule, schedule_len,
-                    stream);  // (the counters only: no room for the staged pre-selection)
+  rc = fused_impl(q, q_rows, group_size, x, x_out, y, y_rows, score, score_len, dense_kv_indptr, sparse_kv_indptr,
+                  dense_kv_indices, dense_kv_indices_len, sparse_kv_indices, sparse_kv_indices_len, eff_batch_size,
+                  topk_val, reserved_bos, reserved_eos, max_num_pages, head_dim, counters, kStaticInts, mode, nullptr,
+                  schedule, schedule_len, stream);
+  if (rc == VTX_E_LAUNCH) {  // a launch that did not run may leave counters behind: clear before the next call
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    g_scratch_dirty[dev] = true;
+  }
+  return rc;
+}
+
+extern "C" int vtx_indexer_fused_noalloc_reset(void* stream) {
+  vtx::clear_error();
+  int32_t* counters = nullptr;
+  int dev = -1;
+  return static_counters(vtx::as_stream(stream), true, &counters, &dev);
 }

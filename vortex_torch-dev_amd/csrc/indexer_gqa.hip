@@ -480,6 +480,7 @@ int gqa_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint16
     cma.nnz = cms->nnz;
     cma.heads = cms->heads;
     cma.page = cms->page_size;
+    cma.page_shift = vtx::log2_exact(cms->page_size);
   }
   const vtx::CmArgs* cmp = cm_launch ? &cma : nullptr;
   if (max_num_pages <= 256) return launch_g<256>(a, cmp, eff_batch_size, lds, s);

@@ -303,6 +303,7 @@ extern "C" int vtx_page_reduce(const uint16_t* x, int64_t x_rows, int32_t rows_p
   a.nnz = nnz;
   a.heads = num_kv_heads;
   a.page = page_size;
+  a.page_shift = vtx::log2_exact(page_size);
   return launch_reduce(a, dim, stream);
 }
 
@@ -331,5 +332,6 @@ extern "C" int vtx_page_reduce_multi(const uint16_t* x, int64_t x_rows, int32_t 
   a.nnz = nnz;
   a.heads = num_kv_heads;
   a.page = page_size;
+  a.page_shift = vtx::log2_exact(page_size);
   return launch_reduce(a, dim, stream);
 }

@@ -25,6 +25,7 @@ struct CmArgs {
   const int64_t* loc;
   int64_t nnz;
   int32_t heads, page;
+  int32_t page_shift;  // log2(page) for a power of two, else -1
 };
 
 // What the in-launch page reduce writes: the mean (CMean) or the max and min
@@ -68,8 +69,8 @@ __device__ __forceinline__ Closing<kLocRegs> closing_build(const CmArgs& cm, con
 #pragma unroll
   for (int j = 0; j < kLocRegs; ++j) {
     const long long e = (long long)j * kWave + lane;
-    const bool closes = e < cm.nnz && (pos[j] + 1) % cm.page == 0;  // C semantics, as page-reduce
-    c.base[j] = closes ? (int)((pos[j] / cm.page) * cm.heads) : -1;
+    const bool closes = e < cm.nnz && divides(pos[j] + 1, cm.page, cm.page_shift);  // C semantics, as page-reduce
+    c.base[j] = closes ? (int)(div_c(pos[j], cm.page, cm.page_shift) * cm.heads) : -1;
     c.mask[j] = __ballot(closes);
     c.count += __popcll(c.mask[j]);
   }

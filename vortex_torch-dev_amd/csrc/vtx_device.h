@@ -130,6 +130,19 @@ __device__ __forceinline__ uint32_t wave_prefix_sum(uint32_t v) {
   return (uint32_t)x;
 }
 
+// C semantics of x / d and of (x % d == 0) for a positive divisor d, given
+// shift = log2(d) when d is a power of two (else -1): shifts and masks then
+// (the quotient truncated toward zero for negative x, as C truncates), the
+// 64-bit division otherwise, which costs a long instruction sequence.
+__device__ __forceinline__ long long div_c(long long x, int d, int shift) {
+  if (shift >= 0) return x >= 0 ? (x >> shift) : -((-x) >> shift);
+  return x / d;
+}
+__device__ __forceinline__ bool divides(long long x, int d, int shift) {
+  if (shift >= 0) return (x & ((1LL << shift) - 1)) == 0;
+  return x % d == 0;
+}
+
 // Value of v in lane `src` (src wave-uniform), read through a scalar register.
 __device__ __forceinline__ uint32_t lane_value(uint32_t v, int src) {
   return (uint32_t)__builtin_amdgcn_readlane((int)v, src);

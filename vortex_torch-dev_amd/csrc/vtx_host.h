@@ -24,6 +24,9 @@ int device_cu_count();
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// log2(d) when d is a power of two, else -1 (the `shift` of vtx::div_c).
+inline int log2_exact(int d) { return d > 0 && (d & (d - 1)) == 0 ? __builtin_ctz((unsigned)d) : -1; }
+
 inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }

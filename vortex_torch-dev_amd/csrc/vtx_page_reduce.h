@@ -24,6 +24,7 @@ struct PageReduceArgs {
   int64_t nnz;
   int32_t heads;
   int32_t page;
+  int32_t page_shift;  // log2(page) for a power of two, else -1
 };
 
 struct Acc {
@@ -86,7 +87,8 @@ __device__ __forceinline__ uint32_t acc_value(const Acc& a, int type, int count)
 // entries e0 .. e0 + kColl - 1 (threads below kColl each look at one; every
 // thread of the block must call this), in loc order, into first_row; returns
 // the page count.  wave_count: LDS scratch of kColl / 64 ints.  Args:
-// PageReduceArgs or any struct with the same loc, nnz, page and heads.
+// PageReduceArgs or any struct with the same loc, nnz, page, page_shift and
+// heads.
 template <int kColl, typename Args>
 __device__ __forceinline__ int collect_pages(const Args& a, long long e0, long long* first_row, int* wave_count) {
   static_assert(kColl % kWave == 0, "whole waves scan loc");
@@ -97,7 +99,7 @@ __device__ __forceinline__ int collect_pages(const Args& a, long long e0, long l
   bool closes = false;
   if ((int)threadIdx.x < kColl && e < a.nnz) {
     pos = a.loc[e];
-    closes = (pos + 1) % a.page == 0;
+    closes = divides(pos + 1, a.page, a.page_shift);
   }
   const uint64_t m = __ballot(closes);
   if (lane == 0 && wave < kColl / kWave) wave_count[wave] = __popcll(m);
@@ -108,7 +110,7 @@ __device__ __forceinline__ int collect_pages(const Args& a, long long e0, long l
     before += (w < wave) ? wave_count[w] : 0;
     total += wave_count[w];
   }
-  if (closes) first_row[before + lanes_below(m)] = (pos / a.page) * a.heads;
+  if (closes) first_row[before + lanes_below(m)] = div_c(pos, a.page, a.page_shift) * a.heads;
   __syncthreads();
   return total;
 }

@@ -567,12 +567,16 @@ __device__ __forceinline__ void bitonic_cx(uint32_t& lo, uint32_t& hi, bool keep
 }
 
 // The wave's 64 * kR values sorted descending (element lane * kR + u).
+// sorted_run (a power of two): the elements already form sorted runs of
+// that length, run r descending for even r and ascending for odd r (what
+// the network's earlier stages leave), so those stages are skipped.
 template <int kR>
-__device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR]) {
+__device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR], int sorted_run = 1) {
   constexpr int N = kWave * kR;
   const int lane = lane_id();
 #pragma unroll
-  for (int k2 = 2; k2 <= N; k2 <<= 1)
+  for (int k2 = 2; k2 <= N; k2 <<= 1) {
+    if (k2 <= sorted_run) continue;  // uniform
 #pragma unroll
     for (int j = k2 >> 1; j > 0; j >>= 1) {
       if (j < kR) {
@@ -589,6 +593,7 @@ __device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR]) {
         }
       }
     }
+  }
 }
 
 // A bitonic sequence of 128 values (element 2 * lane + u) sorted descending.
@@ -648,14 +653,16 @@ __device__ __forceinline__ void merge_lists_bitonic_run(int k, BitonicRunShared<
 // each wave sorts its 64 * kR composites descending (strides below kR inside
 // a lane, the others across lanes) and keeps its best 64, then the lists are
 // merged (merge_lists_bitonic_run).  emit(rank, comp) for rank 0 .. k-1,
-// from wave 0.  Every thread of the workgroup calls it; it contains barriers.
+// from wave 0.  sorted_run: as for wave_sort_desc_run.  Every thread of the
+// workgroup calls it; it contains barriers.
 template <int T, int kR, typename Emit>
-__device__ __forceinline__ void select_bitonic_run(uint32_t (&comp)[kR], int k, BitonicRunShared<T>& bs, Emit emit) {
+__device__ __forceinline__ void select_bitonic_run(uint32_t (&comp)[kR], int k, BitonicRunShared<T>& bs, Emit emit,
+                                                   int sorted_run = 1) {
   static_assert(kR >= 1 && (kR & (kR - 1)) == 0 && 64 % kR == 0, "kR: a power of two dividing 64");
   constexpr int kWaves = T / kWave;
   const int lane = lane_id();
   const int wave = uniform(threadIdx.x / kWave);
-  wave_sort_desc_run<kR>(comp);
+  wave_sort_desc_run<kR>(comp, sorted_run);
   if constexpr (kWaves == 1) {
 #pragma unroll
     for (int u = 0; u < kR; ++u)

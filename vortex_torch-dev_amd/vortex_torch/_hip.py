@@ -65,6 +65,8 @@ _SIGNATURES = {
          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp],
         ctypes.c_int,
     ),
+    "vtx_indexer_fused_workspace_len": ([_i32], ctypes.c_int64),
+    "vtx_indexer_fused_noalloc_reset": ([_vp], ctypes.c_int),
     "vtx_indexer_fused_supported": ([_i32], ctypes.c_int),
     "vtx_indexer_fused_cmean": (
         [_vp, _i64, _i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64,
@@ -122,6 +124,8 @@ _SIGNATURES = {
     "vtx_paged_decode_attention_supported": ([_i32, _i32], ctypes.c_int),
     "vtx_bf16_rounding_check": ([_vp, _vp], ctypes.c_int),
     "vtx_stream_capture_id": ([_vp, ctypes.POINTER(ctypes.c_ulonglong)], ctypes.c_int),
+    "vtx_probe_read": ([_vp, _i64, _vp, _i64, ctypes.c_uint32, _vp], ctypes.c_int),
+    "vtx_probe_gather": ([_vp, _i64, _i32, _vp, _i64, _vp, _i32, _vp, _i64, ctypes.c_uint32, _vp], ctypes.c_int),
     "vtx_segment_scan": (
         [_i32, ctypes.c_float, _vp, _i64, _i32, _vp, _i32, _i32, _i32, _i32, _vp],
         ctypes.c_int,
@@ -558,6 +562,26 @@ def indexer_fused_supported(head_dim: int) -> bool:
     return bool(load_library().vtx_indexer_fused_supported(int(head_dim)))
 
 
+def indexer_fused_workspace_len(segments: int) -> int:
+    """int32 entries of a fused-indexer workspace (arrival counters and the
+    staging zone of the split layout's pre-selection) that serves every call
+    with up to `segments` segments; allocate it zeroed."""
+    n = int(load_library().vtx_indexer_fused_workspace_len(int(segments)))
+    if n < 0:
+        raise RuntimeError(f"vortex_torch: no fused-indexer workspace for {segments} segments")
+    return n
+
+
+def indexer_fused_noalloc_reset(device=None) -> None:
+    """Clears the arrival counters of the no-allocation entry point's
+    workspace on `device` (a fill kernel on its current stream)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    lib = load_library()
+    with _on_device(dev):
+        rc = lib.vtx_indexer_fused_noalloc_reset(_stream(dev))
+    _check(rc, "indexer_fused_noalloc_reset")
+
+
 def _schedule_args(schedule):
     """(pointer, length) of a planner-written fused schedule, or (None, 0)."""
     if schedule is None:
@@ -592,9 +616,11 @@ def indexer_fused(
     q: bf16 [S, G, D] (the head-group mean is taken in the kernel and written
     to x_out if given) or [S, 1, D] / [S, D] already-averaged rows (G taken as
     0: rows used as they are).  y: centroid pool [rows, 1, D]; score: the GeMV
-    output buffer; the block tables come from the planner.  seg_counters: an
-    int32 buffer of at least S zeros that lets long segments be split over
-    several workgroups (the kernel leaves it zeroed); mode: FUSED_AUTO,
+    output buffer; the block tables come from the planner.  seg_counters: the
+    split layout's int32 workspace, zeroed once (``indexer_fused_workspace_len``
+    entries for up to S segments, or at least S for counters only), that
+    lets long segments be split over several workgroups (the kernel leaves
+    its counters at zero); mode: FUSED_AUTO,
     FUSED_SEGMENT or FUSED_SPLIT.  cmean: (k_cache [rows, P, D] bf16, loc
     int64, num_kv_heads) — the layer's page-finish mean into y, run first in
     the same launch (``vtx_indexer_fused_cmean``), with the results of a
@@ -602,7 +628,7 @@ def indexer_fused(
     fused_schedule plan_decode wrote for this block table (the workgroup
     order of the one-workgroup-per-segment layout; speed only).  noalloc:
     launch through ``vtx_indexer_fused_noalloc`` (the library's own
-    counters; no seg_counters, no cmean).
+    workspace; no seg_counters, no cmean).
     """
     lib = load_library()
     tensors = [q, y, score, dense_kv_indptr, sparse_kv_indptr, dense_kv_indices, sparse_kv_indices]
@@ -1009,3 +1035,31 @@ def bf16_rounding_check(device="cuda") -> tuple:
         _check(lib.vtx_bf16_rounding_check(counts.data_ptr(), _stream(dev)), "bf16_rounding_check")
     c = counts.cpu()
     return int(c[0]), int(c[1])
+
+
+def probe_read(src: torch.Tensor, sink: torch.Tensor, magic: int = 0x5a17c0de) -> None:
+    """Sequential read of every byte of `src` (bandwidth probe; see
+    include/vortex_hip.h); sink: int32 scratch, left as it was."""
+    dev = _require_gpu(src, sink)
+    lib = load_library()
+    with _on_device(dev):
+        rc = lib.vtx_probe_read(src.data_ptr(), src.numel() * src.element_size(), sink.data_ptr(), sink.numel(),
+                                magic, _stream(dev))
+    _check(rc, "probe_read")
+
+
+def probe_gather(pool: torch.Tensor, rows: torch.Tensor, sink: torch.Tensor, indptr=None,
+                 magic: int = 0x5a17c0de) -> None:
+    """Reads the rows `rows` (int32) of `pool` ([R, ..] bf16, 256- or
+    1152-byte rows) in the indexer's scoring passes (bandwidth probe); with
+    `indptr` every workgroup first waits for one load of it."""
+    dev = _require_gpu(pool, rows, sink)
+    _req(rows, torch.int32, "rows")
+    row_bytes = pool[0].numel() * pool.element_size()
+    lib = load_library()
+    with _on_device(dev):
+        rc = lib.vtx_probe_gather(pool.data_ptr(), pool.shape[0], row_bytes, rows.data_ptr(), rows.numel(),
+                                  indptr.data_ptr() if indptr is not None else None,
+                                  (indptr.numel() - 1) if indptr is not None else 0, sink.data_ptr(), sink.numel(),
+                                  magic, _stream(dev))
+    _check(rc, "probe_gather")

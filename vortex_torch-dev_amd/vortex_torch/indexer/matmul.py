@@ -44,7 +44,7 @@ class PendingGemv(_deferred.Pending):
     def fuse_with_topk(self, o: torch.Tensor, ctx: Context,
                        seg_counters: Optional[torch.Tensor] = None) -> None:
         """q-mean (if recorded) + GeMV + topK into ``o`` in one kernel.
-        ``seg_counters`` (the topK op's zeroed int32 buffer, one entry per
+        ``seg_counters`` (the topK op's zeroed int32 workspace, one counter per
         segment) lets the kernel split long segments over several workgroups."""
         sc = _deferred.current_scope()
         mean = _deferred.pending_of(self.x)

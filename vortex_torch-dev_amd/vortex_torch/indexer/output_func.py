@@ -26,9 +26,6 @@ from ..abs import FORMAT, vOp, vTensor
 from .context import Context
 from .matmul import PendingGemm, PendingGemv, _schedule_of
 
-_STAGE_INT32_PER_SEGMENT = 8 * 64 * 2  # the fused kernel's staged lists (kStageLists of 64 uint64)
-_STAGE_MAX_SEGMENTS = 512              # larger batches take the one-workgroup-per-segment layout
-
 
 class topK(vOp):
     _impl_map: Dict[FORMAT, Callable] = {
@@ -38,8 +35,9 @@ class topK(vOp):
     def __init__(self):
         super().__init__()
         self.impl: Optional[Callable] = None
-        # arrival counters of the fused kernel's split layout, one per segment
-        # the block table can hold; zero between launches
+        # workspace of the fused kernel's split layout: an arrival counter per
+        # segment the block table can hold (zero between launches) and the
+        # staging zone of its pre-selection
         self.seg_counters: Optional[torch.Tensor] = None
 
     def profile(self, x: vTensor, o: vTensor, ctx: Context) -> None:
@@ -58,12 +56,11 @@ class topK(vOp):
             f"{p}x and o must be on the same device (x.device={x.device}, o.device={o.device})")
         indptr = ctx.dense_kv_indptr
         if isinstance(indptr, torch.Tensor) and indptr.numel() > 1 and x.device.type == "cuda":
-            # one arrival counter per segment, then (for batches few enough in
-            # segments for the split layout) room for its staged pre-selection:
-            # 8 lists of 64 (composite, row id) pairs per segment
+            # one arrival counter per segment and the staging zone, sized by
+            # the library for every batch the block table can hold
             S = indptr.numel() - 1
-            stage = S * _STAGE_INT32_PER_SEGMENT + 2 if S <= _STAGE_MAX_SEGMENTS else 0
-            self.seg_counters = torch.zeros((S + stage,), dtype=torch.int32, device=x.device)
+            self.seg_counters = torch.zeros((_hip.indexer_fused_workspace_len(S),), dtype=torch.int32,
+                                            device=x.device)
 
     def execute(self, x: torch.Tensor, o: torch.Tensor, ctx: Context) -> torch.Tensor:
         assert self.impl is not None, f"{self._prefix()}execute called before profile() (impl is None)"
