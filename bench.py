@@ -12,7 +12,10 @@ stream and `value` is their median in µs (min, max and mean in replay_us).
 
 Extra fields: achieved_GBps (algorithmic bytes of the step / time); roofline
 (the fused indexer kernel — the dominant one — timed alone from a graph of
-its 27 per-layer launches, at least 50 replays, median per launch);
+its 27 per-layer launches, at least 50 replays, median per launch; with the
+box's ceiling beside it: a bare gather of the same rows, the same gather
+behind one dependent load of the segment bounds, and a sequential read of
+1 GiB, as achievable_GBps, frac_of_achievable, ceiling and seq_read);
 unfused_us_per_step (the same step with every op launched separately,
 VORTEX_FUSE=0); cpu_baseline (the CPU oracle on the same step, one thread
 per host core, median of 3 runs); configs (C3, C4 and C5 measured the same
@@ -28,7 +31,10 @@ Other invocations:
                      (with --probe-unfused also the step with every op on its
                      own; at C4 the burst), then a bf16 negation of a 512 MiB
                      buffer (a copy kernel of known size), and exits: the
-                     program the counter passes (rocprofv3 --pmc) profile.
+                     program the counter passes (rocprofv3 --pmc) profile;
+  --traffic-from DIR turns those passes into profiles/traffic.json, which the
+                     roofline's `traffic` reads (only while the kernel, its
+                     algorithmic bytes and the kernel sources still match).
   --attention        paged decode attention over the sparse table the indexer
                      selects and over the dense table (all pages), per layer;
   --flow gqa / quest the same decode step with gqa_block_sparse_attention or
@@ -36,7 +42,7 @@ Other invocations:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
                        [--config c2|c3|c4|c5] [--flow block_sparse|gqa|quest] [--attention]
-                       [--layers N] [--traffic-probe [--probe-unfused]]
+                       [--layers N] [--traffic-probe [--probe-unfused]] [--traffic-from DIR]
 """
 from __future__ import annotations
 
@@ -59,14 +65,49 @@ import workloads as W  # noqa: E402
 METRIC = json.load(open(os.path.join(ROOT, "BASELINE.json")))["metric"]
 HBM_PEAK_GBPS = 8000.0
 
-# HBM bytes per launch of each configuration's dominant kernel, from the
-# FETCH_SIZE and WRITE_SIZE counter passes over --traffic-probe (each scaled
-# by what the counter reads for the probe's copy kernel of known size: 0.5 for
-# FETCH_SIZE, 1.0 for WRITE_SIZE); the fused indexer launches include the
-# layer's decode CMean.  C2 17,111 KiB fetched + 466 KiB written per launch,
-# C3 17,107 + 464, C5 13,149 + 143, C4 (one pass of CMean + CMax over the
-# closed K tiles) 1,052,803 + 262,144.
-TRAFFIC_BYTES_PER_LAUNCH = {"c2": 35_498_762, "c3": 36_053_204, "c5": 27_136_366, "c4": 2_424_393_466}
+# HBM bytes per launch of each configuration's dominant kernel come from the
+# FETCH_SIZE and WRITE_SIZE counter passes over --traffic-probe, each scaled
+# by what the counter reads for the probe's copy kernel of known size;
+# `--traffic-from DIR` turns those passes into profiles/traffic.json, keyed by
+# configuration, with the kernel's name, its algorithmic bytes and a hash of
+# the kernel sources.  A run uses a figure only when all three match its own
+# (kernel_sources_hash below); otherwise `traffic` is null and
+# `traffic_note` says why, so a kernel change cannot leave a stale figure.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def kernel_sources_hash() -> str:
+    """sha256 (first 16 hex digits) of every kernel source and header."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "vortex_torch-dev_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def traffic_for(cfg: str, kernel: str, bytes_per_launch: int):
+    """(HBM bytes per launch, None) from profiles/traffic.json when it was
+    measured for this kernel, these algorithmic bytes and these sources;
+    else (None, the reason)."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            rec = json.load(fh).get(cfg)
+    except (OSError, ValueError):
+        return None, "no profiles/traffic.json"
+    if rec is None:
+        return None, f"no counter passes recorded for {cfg}"
+    if rec.get("kernel") != kernel:
+        return None, f"counter passes were of {rec.get('kernel')}, this run launches {kernel}"
+    if rec.get("bytes_per_launch") != bytes_per_launch:
+        return None, f"algorithmic bytes differ from the counter passes' ({rec.get('bytes_per_launch')})"
+    if rec.get("sources") != kernel_sources_hash():
+        return None, "kernel sources changed since the counter passes"
+    return int(rec["traffic"]), None
 
 
 def _parse():
@@ -88,6 +129,8 @@ def _parse():
     ap.add_argument("--probe-unfused", action="store_true",
                     help="with --traffic-probe: also run the step with every op launched on its own")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3 / C4 / C5 keys of the C2 line")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="write profiles/traffic.json from the counter passes under DIR (no GPU needed), exit")
     return ap.parse_args()
 
 
@@ -99,7 +142,8 @@ DECODE_CONFIGS = {
            "(H_q 16, H_kv 8, D 128), page 16, top-30 + 1 BOS + 1 EOS, 40k-page shared pool, "
            "per-layer pools; one HIP graph per step"),
     "c3": ("C3: decode step, batch 8 x 32768 tokens (2048 pages per request), 27 sparse layers, "
-           "H_q 16, H_kv 8, D 128, page 16, top-64 + 1 BOS + 1 EOS; one HIP graph per step"),
+           "H_q 16, H_kv 8, D 128, page 16, top-64 + 1 BOS + 1 EOS; K = N(0,1) noise + per-(page, head) "
+           "offsets ~ N(0, 0.5), centroids = its CMean; one HIP graph per step"),
     "c5": ("C5: MLA latent-cache decode step, batch 32, L~U[4096,16384], 27 sparse layers, "
            "1 latent head, G 16, D 576, page 16, top-32 + 1 BOS + 1 EOS; one HIP graph per step"),
 }
@@ -150,14 +194,24 @@ class DecodeStep:
         self.flows, self.caches, self.qs = [], [], []
         self.plain = []  # (k, centroids, q) without the layout tag
         rows = batch.pool_pages * H
+        # C3: K with per-(page, head) offsets and the centroids its CMean writes;
+        # otherwise K ~ N(0, 1) and centroid rows ~ N(0, 0.25^2), the spread of a
+        # mean of 16 such rows
+        offsets = bool(batch.extra.get("k_page_offsets"))
         for layer in range(layers):
             f = vflow.build_vflow(flow_name)
-            k = W.randn_bf16((rows, P, D), seed + 3 * layer, dev)
+            if offsets:
+                k = W.k_pool(batch, seed + 3 * layer, dev, page_offsets=True)
+            else:
+                k = W.randn_bf16((rows, P, D), seed + 3 * layer, dev)
             qp = W.randn_bf16((B * H, G, D), seed + 3 * layer + 2, dev)
             cache = {"k": as_vtensor(k, FORMAT.PAGED)}
             for j, (name, (r, c)) in enumerate(f.create_cache(P, D).items()):
-                cache[name] = as_vtensor(W.randn_bf16((rows, r, c), seed + 3 * layer + 1 + 101 * j, dev, std=0.25),
-                                         FORMAT.PAGED)
+                if offsets and name == "centroids":
+                    pool = W.centroids_from_k(k, batch)
+                else:
+                    pool = W.randn_bf16((rows, r, c), seed + 3 * layer + 1 + 101 * j, dev, std=0.25)
+                cache[name] = as_vtensor(pool, FORMAT.PAGED)
             cen = cache.get("centroids")
             self.plain.append((k, cen, qp))
             self.flows.append(f)
@@ -207,6 +261,50 @@ class DecodeStep:
                                    b.max_pages_per_request, seg_counters=f.output_func.seg_counters,
                                    mode=fused_layout(), cmean=(k, self.loc, b.num_kv_heads),
                                    schedule=ic._fused_schedule)
+
+
+def gather_ceiling(step: DecodeStep, plan: dict, args) -> dict:
+    """The bare gather of the rows the fused kernel scores, from the same 27
+    per-layer centroid pools (vtx_probe_gather: one coalesced load of a
+    pass's row ids, then the rows, nothing computed), and the same gather
+    with one dependent load of the segment bounds first (the fused kernel's
+    chain of trips); each as a graph of the layers' launches, median per
+    launch of max(50, --kernel-reps) replays."""
+    from vortex_torch import _hip
+
+    b = step.batch
+    dip = plan["dense_indptr"].astype(np.int64)
+    pos = [np.arange(dip[s] + b.bos, dip[s + 1] - b.eos) for s in range(len(dip) - 1)
+           if dip[s + 1] - b.eos - (dip[s] + b.bos) > b.topk]
+    with torch._C.DisableTorchFunctionSubclass():
+        rows = step.ictx.dense_kv_indices[torch.from_numpy(np.concatenate(pos)).to(step.dev)].contiguous()
+        pools = [cen.view(cen.shape[0], -1) for (_, cen, _) in step.plain]
+        indptr = step.ictx.dense_kv_indptr
+    sink = torch.zeros(4 * rows.numel() + 4096, dtype=torch.int32, device=step.dev)  # one entry per thread
+    row_bytes = pools[0].shape[1] * 2
+    nbytes = rows.numel() * (row_bytes + 4)
+    out = {"rows": int(rows.numel()), "row_bytes": int(row_bytes), "bytes_per_launch": int(nbytes)}
+    for key, ip in (("gather", None), ("gather_head", indptr)):
+        g = capture(lambda: [_hip.probe_gather(p, rows, sink, indptr=ip) for p in pools])
+        us = replay_stats(time_replays(g, max(50, args.kernel_reps), 3), per=len(pools))["median"]
+        del g
+        out[f"{key}_us"] = us
+        out[f"{key}_GBps"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    return out
+
+
+def seq_read_ceiling(dev, args) -> dict:
+    """A sequential read of 1 GiB (vtx_probe_read), median of max(20,
+    --kernel-reps) launches: the box's streaming-read rate."""
+    from vortex_torch import _hip
+
+    n = 1 << 30
+    src = torch.empty(n // 2, dtype=torch.int16, device=dev).fill_(1)
+    sink = torch.zeros(4096 * 512, dtype=torch.int32, device=dev)
+    g = capture(lambda: _hip.probe_read(src, sink))
+    us = replay_stats(time_replays(g, max(20, args.kernel_reps), 3))["median"]
+    del g, src
+    return {"bytes": n, "us": us, "GBps": round(n / (us * 1e-6) / 1e9, 1)}
 
 
 def algorithmic_bytes(batch: W.DecodeBatch, plan: dict, layers: int, loc_host: np.ndarray) -> dict:
@@ -372,6 +470,12 @@ def measure_decode(cfg: str, args, dev, unfused: bool = False, cpu: bool = False
     us_fused = kern["median"]
     fused_gbps = nbytes["fused"] / (us_fused * 1e-6) / 1e9
     print(f"[bench] {cfg} fused indexer {us_fused:.2f} us/launch, {fused_gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    ceil = gather_ceiling(step, plan, args)
+    print(f"[bench] {cfg} bare gather of the same rows {ceil['gather_us']:.2f} us/launch "
+          f"({ceil['gather_GBps']:.0f} GB/s), with the bounds trip first {ceil['gather_head_us']:.2f} us",
+          file=sys.stderr, flush=True)
+    kname = fused_kernel_name(batch)
+    traffic, note = traffic_for(cfg, kname, nbytes["fused"])
     res = {
         "workload": DECODE_CONFIGS[cfg],
         "us_per_step": st,
@@ -383,18 +487,26 @@ def measure_decode(cfg: str, args, dev, unfused: bool = False, cpu: bool = False
         "algorithmic_bytes_per_step": nbytes["step"],
         "achieved_GBps": round(nbytes["step"] / (st["median"] * 1e-6) / 1e9, 1),
         "roofline": {
-            "kernel": f"{fused_kernel_name(batch)} (CMean of the closed pages + q-mean + GeMV + top-k, one layer)",
+            "kernel": f"{kname} (CMean of the closed pages + q-mean + GeMV + top-k, one layer)",
             "bound": "hbm",
             "achieved": round(fused_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(fused_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get(cfg),
+            "traffic": traffic,
             "us_per_launch": us_fused,
             "us_per_launch_stats": kern,
             "bytes_per_launch": nbytes["fused"],
+            # the box's ceiling for this access pattern: a kernel that only
+            # gathers the same rows (vtx_probe_gather), and the fused kernel's
+            # rate as a fraction of it (frac stays against the 8 TB/s peak)
+            "achievable_GBps": round(ceil["gather_GBps"], 1),
+            "frac_of_achievable": round(fused_gbps / ceil["gather_GBps"], 4),
+            "ceiling": ceil,
         },
     }
+    if note:
+        res["roofline"]["traffic_note"] = note
     if unfused:
         os.environ["VORTEX_FUSE"] = "0"
         gu = capture(step.run)
@@ -414,7 +526,7 @@ def measure_decode(cfg: str, args, dev, unfused: bool = False, cpu: bool = False
 def bench_decode(args, dev) -> dict:
     if args.traffic_probe:
         batch = getattr(W, args.config)()
-        return traffic_probe(DecodeStep(batch, args.layers, dev), dev, unfused=args.probe_unfused)
+        return traffic_probe(DecodeStep(batch, args.layers, dev), dev, unfused=args.probe_unfused, cfg=args.config)
     m = measure_decode(args.config, args, dev, unfused=not args.no_unfused, cpu=not args.no_cpu)
     st = m["us_per_step"]
     out = {
@@ -440,6 +552,9 @@ def bench_decode(args, dev) -> dict:
         "unfused_us_per_step": m.get("unfused_us_per_step"),
         "roofline": m["roofline"],
     }
+    out["roofline"]["seq_read"] = seq_read_ceiling(dev, args)
+    print(f"[bench] sequential read of 1 GiB: {out['roofline']['seq_read']['GBps']:.0f} GB/s", file=sys.stderr,
+          flush=True)
     if "cpu_baseline" in m:
         out["cpu_baseline"] = m["cpu_baseline"]
     if args.config == "c2" and not args.no_extra:
@@ -538,13 +653,16 @@ def bench_attention(args, dev) -> dict:
     }
 
 
-def traffic_probe(step: DecodeStep, dev, unfused: bool = False) -> dict:
+def traffic_probe(step: DecodeStep, dev, unfused: bool = False, cfg: str = "c2") -> dict:
     """Kernels for a counter pass: every layer's fused indexer launch (twice:
     the second pass is the one to read, the first warms the code object and
     the TLB like the timed replays), optionally the step with every op
-    launched on its own (GeMV, topK, CMean), then a copy kernel of known size."""
+    launched on its own (GeMV, topK, CMean), then a copy kernel of known size.
+    Returns what --traffic-from needs besides the counters: the kernel's name,
+    its algorithmic bytes per launch and the kernel sources' hash."""
     os.environ["VORTEX_FUSE"] = "1"
     step.run()  # the planner fills the block tables the kernels read
+    nbytes = algorithmic_bytes(step.batch, plan_summary(step), step.layers, step.loc_host)
     with torch._C.DisableTorchFunctionSubclass():
         for _ in range(2):
             step.indexer_kernels_only()
@@ -558,8 +676,64 @@ def traffic_probe(step: DecodeStep, dev, unfused: bool = False) -> dict:
         dst = torch.empty_like(src)
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    return {"probe": "traffic", "fused_kernel": fused_kernel_name(step.batch), "launches": 2 * step.layers,
+    return {"probe": "traffic", "config": cfg, "kernel": fused_kernel_name(step.batch),
+            "bytes_per_launch": nbytes["fused"], "sources": kernel_sources_hash(), "launches": 2 * step.layers,
             "copy_kernel": "neg (bf16)", "copy_read_bytes": 2 * n, "copy_write_bytes": 2 * n}
+
+
+def traffic_from(pmc_dir: str) -> dict:
+    """profiles/traffic.json from the counter passes under pmc_dir: for each
+    configuration, <cfg>_fetch/ and <cfg>_write/ (rocprofv3 --pmc FETCH_SIZE,
+    then WRITE_SIZE, --output-format csv, over --traffic-probe) and
+    probe_<cfg>.json (that program's output line).  HBM bytes per launch =
+    the median over the kernel's dispatches of FETCH_SIZE / f + WRITE_SIZE / w
+    (KiB), with f and w what the counters read for the probe's copy kernel
+    per byte it reads and writes."""
+    import csv
+    import glob
+    import statistics
+
+    def per_dispatch(path, counter):
+        sums = {}
+        for fn in glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(fn)):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (r["Kernel_Name"], r["Dispatch_Id"])
+                sums[key] = sums.get(key, 0.0) + float(r["Counter_Value"])
+        return sums
+
+    def short(name):
+        name = name.replace("void ", "").replace("(anonymous namespace)::", "")
+        return name[:name.index(">") + 1] if "<" in name else name.split("(")[0]
+
+    out = {}
+    for cfg in ("c2", "c3", "c5", "c4"):
+        probe_file = os.path.join(pmc_dir, f"probe_{cfg}.json")
+        if not os.path.exists(probe_file):
+            continue
+        probe = json.loads(open(probe_file).read().strip().splitlines()[-1])
+        fetch = per_dispatch(os.path.join(pmc_dir, f"{cfg}_fetch"), "FETCH_SIZE")
+        write = per_dispatch(os.path.join(pmc_dir, f"{cfg}_write"), "WRITE_SIZE")
+        copy_f = [v for (k, _), v in fetch.items() if "neg" in k]
+        copy_w = [v for (k, _), v in write.items() if "neg" in k]
+        f = copy_f[-1] * 1024.0 / probe["copy_read_bytes"]
+        w = copy_w[-1] * 1024.0 / probe["copy_write_bytes"]
+        fk = [v for (k, _), v in fetch.items() if short(k) == probe["kernel"]]
+        wk = [v for (k, _), v in write.items() if short(k) == probe["kernel"]]
+        if not fk or not wk:
+            raise SystemExit(f"{cfg}: no dispatches of {probe['kernel']} in the counter passes")
+        traffic = statistics.median(fk) * 1024.0 / f + statistics.median(wk) * 1024.0 / w
+        out[cfg] = {"kernel": probe["kernel"], "bytes_per_launch": probe["bytes_per_launch"],
+                    "sources": probe["sources"], "traffic": int(round(traffic)),
+                    "traffic_over_algorithmic": round(traffic / probe["bytes_per_launch"], 4),
+                    "fetch_KiB_per_dispatch": round(statistics.median(fk), 1),
+                    "write_KiB_per_dispatch": round(statistics.median(wk), 1),
+                    "fetch_factor": round(f, 4), "write_factor": round(w, 4), "dispatches": len(fk)}
+    with open(TRAFFIC_FILE, "w") as fh:
+        json.dump(out, fh, indent=1)
+        fh.write("\n")
+    return out
 
 
 def bench_burst(args, dev) -> dict:
@@ -608,8 +782,9 @@ def bench_burst(args, dev) -> dict:
         src = torch.ones(n, dtype=torch.bfloat16, device=dev)
         torch.neg(src, out=torch.empty_like(src))
         torch.cuda.synchronize()
-        return {"probe": "traffic", "config": "c4", "copy_kernel": "neg (bf16)", "copy_read_bytes": 2 * n,
-                "copy_write_bytes": 2 * n}
+        return {"probe": "traffic", "config": "c4", "kernel": "reduce_rows_vec_kernel<16, 3>",
+                "bytes_per_launch": fused_bytes, "sources": kernel_sources_hash(), "copy_kernel": "neg (bf16)",
+                "copy_read_bytes": 2 * n, "copy_write_bytes": 2 * n}
     st = replay_stats(time_replays(capture(fused), args.steps, args.warmup))
     us_fused = st["median"]
     us_sep = replay_stats(time_replays(capture(separate), max(10, args.steps // 2), 3))["median"]
@@ -617,7 +792,8 @@ def bench_burst(args, dev) -> dict:
     print(f"[bench] C4 fused {us_fused:.1f} us ({gbps:.0f} GB/s), separate {us_sep:.1f} us",
           file=sys.stderr, flush=True)
     need = 1 | 2  # Sum | Max statistics
-    return {
+    c4_traffic, c4_note = traffic_for("c4", f"reduce_rows_vec_kernel<16, {need}>", fused_bytes)
+    out = {
         "metric": "us per page-finish burst (CMean + CMax) and achieved HBM GB/s",
         "value": round(us_fused, 2),
         "unit": "us/burst",
@@ -644,15 +820,21 @@ def bench_burst(args, dev) -> dict:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": TRAFFIC_BYTES_PER_LAUNCH.get("c4"),
+            "traffic": c4_traffic,
             "us_per_launch": us_fused,
             "bytes_per_launch": fused_bytes,
         },
     }
+    if c4_note:
+        out["roofline"]["traffic_note"] = c4_note
+    return out
 
 
 def main():
     args = _parse()
+    if args.traffic_from:
+        print(json.dumps(traffic_from(args.traffic_from)))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
                                    "(the indexer shards by request / kv head with no exchange)"}))

@@ -281,6 +281,61 @@ def test_flow_end_to_end_against_oracle(gpu):
     np.testing.assert_array_equal(_np(run.ic.sparse_kv_indices), sel)
 
 
+def test_c3_configured_inputs_cmean_then_fused_indexer(gpu):
+    """C3 with the inputs its configuration names: K = N(0, 1) noise plus a
+    per-(page, head) offset ~ N(0, 0.5), the centroid pool written by the
+    package's CMean over every page, then plan and the fused indexer at full
+    size (64 segments of 2046 middle pages: the split layout with the topK
+    op's workspace).  CMean within tolerance of the oracle on a sample of
+    pages; every covered score within tolerance of the oracle's GeMV; the
+    selection the oracle's top-k of the GPU's scores, bit for bit."""
+    dev = gpu
+    batch = W.c3()
+    assert batch.extra.get("k_page_offsets")
+    ic, _ = W.make_contexts(batch, dev)
+    _plan(batch, ic, dev)
+    H, G, D, P = batch.num_kv_heads, batch.group_size, batch.head_dim, batch.page_size
+    S = batch.batch * H
+    k = W.k_pool(batch, 11, dev, page_offsets=True)
+    cen = W.centroids_from_k(k, batch)
+    rng = np.random.default_rng(3)
+    pages = rng.choice(batch.pool_pages, 256, replace=False)
+    srows = (pages[:, None] * H + np.arange(H)[None, :]).reshape(-1)
+    sel_rows = torch.as_tensor(srows, device=dev)
+    xs = _bits(k[sel_rows]).reshape(len(srows), P, D)
+    exp, _ = O.page_reduce(xs, np.zeros((len(srows), 1, D), np.uint16), np.arange(len(pages)) * P + (P - 1), H, P,
+                           1, O.MEAN)
+    got = _bits(cen[sel_rows]).reshape(len(srows), 1, D)
+    np.testing.assert_allclose(O.bf16_to_f32(got), O.bf16_to_f32(exp), rtol=1e-2, atol=1e-3)
+    del k
+
+    q = W.randn_bf16((S, G, D), 12, dev)
+    qm = torch.full((S, 1, D), 3.0, device=dev, dtype=torch.bfloat16)
+    sc = torch.full((ic.dense_kv_indices.numel(), 1, 1), -5.0, device=dev, dtype=torch.bfloat16)
+    sp = ic.sparse_kv_indices.clone()
+    ws = torch.zeros(_hip.indexer_fused_workspace_len(S), dtype=torch.int32, device=dev)
+    _hip.indexer_fused(q, qm, cen, sc, ic.dense_kv_indptr, ic.sparse_kv_indptr, ic.dense_kv_indices, sp, S,
+                       batch.topk, batch.bos, batch.eos, batch.max_pages_per_request, seg_counters=ws,
+                       mode=_hip.FUSED_AUTO)
+    torch.cuda.synchronize()
+    ref = O.plan_decode(_np(batch.seq_lens), _np(batch.req_to_token), _np(batch.req_indices), P, H, batch.topk,
+                        batch.bos, batch.eos, batch.max_chunk)
+    qm_exp = O.q_group_mean(_bits(q).reshape(S, G, D))
+    np.testing.assert_array_equal(_bits(qm).reshape(qm_exp.shape), qm_exp)
+    sc_exp, cov = O.gemv(qm_exp, _bits(cen).reshape(cen.shape), ref["dense_indices"], ref["winfo_q"],
+                         ref["winfo_off"], ref["winfo_len"], ref["num_workloads"], sc.numel())
+    got_sc = _bits(sc)
+    np.testing.assert_allclose(O.bf16_to_f32(got_sc)[cov], O.bf16_to_f32(sc_exp)[cov], rtol=1e-2, atol=1e-3)
+    sel, _ = O.topk(got_sc, ref["dense_indptr"], ref["sparse_indptr"], ref["dense_indices"], ref["sparse_indices"],
+                    S, batch.topk, batch.bos, batch.eos)
+    np.testing.assert_array_equal(_np(sp), sel)
+    # the offsets separate the pages: a segment's best score stands well above its median
+    f = O.bf16_to_f32(got_sc)
+    dip = ref["dense_indptr"]
+    spread = [np.max(f[dip[s] + 1:dip[s + 1] - 1]) - np.median(f[dip[s] + 1:dip[s + 1] - 1]) for s in range(S)]
+    assert min(spread) > 0.0
+
+
 @pytest.mark.parametrize("name", ["c2", "c3"])
 def test_flow_graph_replay(gpu, name):
     # C2 runs one workgroup per segment, C3 (64 segments) the split layout

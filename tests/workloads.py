@@ -114,8 +114,11 @@ def c2(seed: int = 1) -> DecodeBatch:
 
 
 def c3(seed: int = 2) -> DecodeBatch:
+    """C3: 8 x 32k tokens, top-64.  extra["k_page_offsets"]: its K pool carries
+    a per-(page, head) offset ~ N(0, 0.5) over N(0, 1) noise (k_pool) and its
+    centroids are that pool's CMean (centroids_from_k), as configured."""
     return make_batch([32768] * 8, pool_pages=20000, seed=seed, num_kv_heads=8, group_size=2,
-                      head_dim=128, topk=64, bos=1, eos=1, row_tokens=32768)
+                      head_dim=128, topk=64, bos=1, eos=1, row_tokens=32768, extra={"k_page_offsets": True})
 
 
 def c5(seed: int = 4) -> DecodeBatch:
@@ -244,6 +247,19 @@ def k_pool(batch: DecodeBatch, seed: int, device, page_offsets: bool = False) ->
                           device=device, dtype=torch.float32) * (0.5 ** 0.5)
         k.add_(off)
     return k.to(torch.bfloat16)
+
+
+def centroids_from_k(k: torch.Tensor, batch: DecodeBatch) -> torch.Tensor:
+    """The centroid pool [pool_pages * H, 1, D] bf16 of a K pool: the package's
+    CMean (the page-reduce kernel) over every page of the pool, one loc entry
+    per page (its last slot), as the cache side writes them page by page."""
+    from vortex_torch import _hip
+
+    H, P, D = batch.num_kv_heads, batch.page_size, batch.head_dim
+    cen = torch.zeros((batch.pool_pages * H, 1, D), device=k.device, dtype=torch.bfloat16)
+    loc = torch.arange(batch.pool_pages, device=k.device, dtype=torch.int64) * P + (P - 1)
+    _hip.page_reduce(k, cen, loc, H, P, 1, _hip.REDUCE_MEAN)
+    return cen
 
 
 def cmean_case(name: str):
