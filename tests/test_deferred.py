@@ -276,18 +276,61 @@ def test_carry_across_a_capture_boundary_is_an_error(carry_launches, monkeypatch
     state["id"] = 0  # ... which ended without launching it
     with pytest.raises(RuntimeError, match="recorded during a graph capture and would now be launched outside"):
         layer.indexer_step()
+    assert _deferred.current_carry() is not None  # kept: it can still run where it belongs
+    _deferred.discard_carry()
     layer.cache_step()  # recorded outside any capture ...
     state["id"] = 9  # ... found inside one
     with pytest.raises(RuntimeError, match="recorded outside any graph capture and would now be launched during"):
         layer.indexer_step()
+    state["id"] = 0  # back outside: the kept carry launches
+    _deferred.flush_carry()
+    assert carry_launches[-1] == "page_reduce"
+    carry_launches.clear()
     state["id"] = 3
     layer.cache_step()
     state["id"] = 4  # another capture
     with pytest.raises(RuntimeError, match="in another capture"):
         _deferred.flush_carry()
+    _deferred.discard_carry()
     assert "page_reduce" not in carry_launches  # never launched where it does not belong
     state["id"] = 6
     layer.cache_step()
     carry_launches.clear()
     layer.indexer_step()  # same capture: consumed
     assert carry_launches == ["indexer_fused+cmean"]
+
+
+def test_capture_hooks_only_while_carrying(carry_launches):
+    """torch.cuda.CUDAGraph's capture methods are wrapped only once a mean is
+    carried, and switching the carry off launches it and restores them."""
+    graph = torch.cuda.CUDAGraph
+    _deferred.remove_capture_hooks()  # (earlier tests carried means)
+    assert not _deferred.capture_hooks_installed()
+    begin, end = graph.capture_begin, graph.capture_end  # torch's own
+    layer = _Layer()
+    layer.cache_step()
+    assert _deferred.capture_hooks_installed() and graph.capture_begin is not begin
+    try:
+        _deferred.set_fusion(carry_cmean=False)
+        assert carry_launches[-1] == "page_reduce" and _deferred.current_carry() is None
+        assert not _deferred.capture_hooks_installed()
+        assert graph.capture_begin is begin and graph.capture_end is end
+        layer.cache_step()  # the carry is off: launched when forward_cache returns
+        assert _deferred.current_carry() is None and carry_launches[-1] == "page_reduce"
+    finally:
+        _deferred.set_fusion()
+
+
+def test_set_fusion_overrides_environment(monkeypatch):
+    monkeypatch.setenv("VORTEX_FUSE", "1")
+    monkeypatch.setenv("VORTEX_FUSE_CMEAN", "1")
+    try:
+        _deferred.set_fusion(fuse=False)
+        assert not _deferred.fusion_enabled() and not _deferred._carry_enabled()
+        _deferred.set_fusion(fuse=True, carry_cmean=False)
+        assert _deferred.fusion_enabled() and not _deferred._carry_enabled()
+        monkeypatch.setenv("VORTEX_FUSE", "0")
+        assert _deferred.fusion_enabled()  # the switch wins over the variable
+    finally:
+        _deferred.set_fusion()
+    assert not _deferred.fusion_enabled()  # handed back to VORTEX_FUSE=0

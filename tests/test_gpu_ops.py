@@ -207,6 +207,13 @@ class _Flow:
         self.flow.forward_indexer(self.q, self.o, self.cache, self.ic)
         self.ic.execute()
         self.cc.execute()
+        # every op's output buffer starts as a finite sentinel, so positions no
+        # workload covers hold defined values when they reach the oracle
+        with torch._C.DisableTorchFunctionSubclass():
+            for op in vars(self.flow).values():
+                buf = getattr(op, "output_buffer", None)
+                if isinstance(buf, torch.Tensor):
+                    buf.fill_(-7.0 if buf.is_floating_point() else -7)
 
     def step(self):
         from vortex_torch.indexer.utils_sglang import plan_decode

@@ -68,8 +68,30 @@ _METADATA = {
 }
 
 
+# Python switches beside the environment variables: None leaves the decision
+# to VORTEX_FUSE / VORTEX_FUSE_CMEAN, True / False override them (set_fusion).
+_switch = {"fuse": None, "carry": None}
+
+
 def fusion_enabled() -> bool:
+    if _switch["fuse"] is not None:
+        return _switch["fuse"]
     return os.environ.get("VORTEX_FUSE", "1") != "0"
+
+
+def set_fusion(fuse: Optional[bool] = None, carry_cmean: Optional[bool] = None) -> None:
+    """Switches of the fused paths, beside VORTEX_FUSE and VORTEX_FUSE_CMEAN:
+    True or False overrides the environment variable, None hands the choice
+    back to it.  ``fuse``: one launch per forward_indexer chain (False: every
+    op launched when called, as the reference does).  ``carry_cmean``: the
+    page-finish mean that forward_cache records is left for the next fused
+    indexer launch (False: it runs when forward_cache returns).  Turning the
+    carry off launches a pending one and removes the graph-capture hooks."""
+    _switch["fuse"] = fuse
+    _switch["carry"] = carry_cmean
+    if not _carry_enabled():
+        flush_carry()
+        remove_capture_hooks()
 
 
 _LAYOUTS = {"auto": 0, "segment": 1, "split": 2}
@@ -172,18 +194,27 @@ def current_scope() -> Optional[Scope]:
 #
 # Graph capture.  A carry belongs to the capture it was recorded in (or to
 # none): it is launched into that capture or, recorded outside any, before a
-# capture starts.  torch.cuda.CUDAGraph.capture_begin and capture_end (which
-# torch.cuda.graph and make_graphed_callables call) launch the carry first, so
-# a capture never ends with a carried mean outside the graph, whatever the
-# order of the flow's calls within it (forward_indexer may precede
-# forward_cache: the last layer's carry then lands at the end of the graph).
-# A carry found on a stream whose capture state has changed by other means
-# (a capture begun or ended outside these two methods) is an error, raised
-# instead of launching the mean outside the work it belongs to.
+# capture starts.  Once a mean has been carried, torch.cuda.CUDAGraph's
+# capture_begin and capture_end (which torch.cuda.graph and
+# make_graphed_callables call) launch the carry first, so a capture never
+# ends with a carried mean outside the graph, whatever the order of the
+# flow's calls within it (forward_indexer may precede forward_cache: the last
+# layer's carry then lands at the end of the graph).  These two hooks are
+# installed with the first carry and removed by remove_capture_hooks() or by
+# switching the carry off (set_fusion(carry_cmean=False)); a process that
+# never carries keeps torch's own methods.  A carry found on a stream whose
+# capture state has changed by other means (a capture begun or ended outside
+# these two methods) is an error, raised instead of launching the mean
+# outside the work it belongs to; the carry then stays recorded
+# (discard_carry() drops it).
 
 
 def _carry_enabled() -> bool:
-    return fusion_enabled() and os.environ.get("VORTEX_FUSE_CMEAN", "1") != "0"
+    if not fusion_enabled():
+        return False
+    if _switch["carry"] is not None:
+        return _switch["carry"]
+    return os.environ.get("VORTEX_FUSE_CMEAN", "1") != "0"
 
 
 def current_carry():
@@ -216,15 +247,26 @@ def _check_capture(carry) -> None:
 
 
 def flush_carry() -> None:
-    """Launches the carried page-finish mean, if any, on its own stream."""
+    """Launches the carried page-finish mean, if any, on its own stream.
+    When the stream's capture state is no longer the one it was recorded in,
+    this raises and the mean stays recorded: it can still be launched once
+    that state is back, or dropped with discard_carry()."""
     c = current_carry()
     if c is None:
         return
-    _tls.carry = None
     _check_capture(c)
+    _tls.carry = None
     pending, stream, _ = c
     with (torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()):
         pending.flush()
+
+
+def discard_carry() -> None:
+    """Drops the carried page-finish mean without launching it (after
+    flush_carry raised for a capture that will not come back).  The centroid
+    or envelope rows of the pages it would have closed then keep their old
+    values until a page-finish reduction over those pages runs again."""
+    _tls.carry = None
 
 
 def _storages(obj, out):
@@ -312,6 +354,7 @@ def scope(active: bool, kind: str = "indexer"):
                     and getattr(sc.pending[0], "carryable", lambda: False)()):
                 p = sc.pending.pop()
                 st = _stream_of(p.x.device)
+                _install_capture_hooks()  # (only while something is carried)
                 _tls.carry = (p, st, _capture_of(st))
             sc.flush()
             if kind == "indexer":
@@ -448,13 +491,20 @@ def _install_launch_hook() -> None:
     _hip.set_pre_launch_hook(flush_carry)
 
 
+_hooked = None  # (CUDAGraph class, original capture_begin, original capture_end) while the hooks are in
+
+
 def _install_capture_hooks() -> None:
     """Makes torch.cuda.CUDAGraph.capture_begin / capture_end launch the carry
-    first (see "Graph capture" above)."""
+    first (see "Graph capture" above).  Installed when a mean is first
+    carried, so a process that never carries one (VORTEX_FUSE_CMEAN=0,
+    set_fusion(carry_cmean=False) or no forward_cache) keeps torch's own
+    methods; remove_capture_hooks() puts those back."""
+    global _hooked
     import functools
 
     graph = getattr(torch.cuda, "CUDAGraph", None)
-    if graph is None or getattr(graph, "_vortex_carry_hooks", False):
+    if graph is None or _hooked is not None:
         return
     begin, end = graph.capture_begin, graph.capture_end
 
@@ -469,8 +519,23 @@ def _install_capture_hooks() -> None:
         return end(self, *args, **kwargs)
 
     graph.capture_begin, graph.capture_end = capture_begin, capture_end
-    graph._vortex_carry_hooks = True
+    _hooked = (graph, begin, end)
+
+
+def remove_capture_hooks() -> None:
+    """Restores torch.cuda.CUDAGraph's own capture_begin / capture_end (a
+    pending carry is launched first)."""
+    global _hooked
+    if _hooked is None:
+        return
+    flush_carry()
+    graph, begin, end = _hooked
+    graph.capture_begin, graph.capture_end = begin, end
+    _hooked = None
+
+
+def capture_hooks_installed() -> bool:
+    return _hooked is not None
 
 
 _install_launch_hook()
-_install_capture_hooks()
