@@ -648,7 +648,8 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   // this work id's share of the CMean tiles (after its scores are counted in)
   auto cm_tiles = [&]() {
     if constexpr (cm_on) {
-      if (w * kWaves < (long long)n_close * cma.heads)  // uniform: tiles w * waves + wave, + grid * waves, ...
+      // uniform: units (tiles, or parts of wide tiles) w * waves + wave, + grid * waves, ...
+      if (w * kWaves < (long long)n_close * cma.heads * vtx::tile_parts<LPR * VPL>())
         vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(cma, closing, (int)(w * kWaves) + wave,
                                                        (int)gridDim.x * kWaves);
     }

@@ -207,11 +207,12 @@ __device__ __forceinline__ void tile_reduce_any(const CmArgs& cm, long long row,
           v[u] = r0 + u < R ? ld16_stream(tile + (long long)(r0 + u) * C + cv * 8) : U4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int u = 0; u < kRowBatch; ++u) {
-          if (r0 + u >= R) break;
-          float f[8];
-          unpack8(v[u], f);
+          if (r0 + u < R) {  // uniform (no break: the loads stay in registers)
+            float f[8];
+            unpack8(v[u], f);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc_add<kNeed>(acc[e], f[e]);
+            for (int e = 0; e < 8; ++e) acc_add<kNeed>(acc[e], f[e]);
+          }
         }
       }
       if constexpr (kKind == kCentroid) {
@@ -224,16 +225,74 @@ __device__ __forceinline__ void tile_reduce_any(const CmArgs& cm, long long row,
   }
 }
 
-// Tiles first, first + stride, ... of the closed pages reduced as the
-// page-reduce launch for rows of kNV 16-byte vectors would (tile_reduce_any);
-// for kernels whose scoring layout is not the tile layout.  Wave-level.
+// Columns blk * 64 + lane of tile `row` for rows of kNV 16-byte vectors that
+// are not a tile_reduce_vec width: each lane sums its column vector's rows in
+// order from 0 (reduce_colvec_kernel's arithmetic), its loads issued
+// kColRows rows at a time (one memory trip for pages of up to kColRows
+// tokens).  Wave-level; the tile must be in range.
+constexpr int kColRows = 16;
+
+template <int kNV, int kKind>
+__device__ __forceinline__ void tile_reduce_colvec_part(const CmArgs& cm, long long row, int blk, uint16_t* dst,
+                                                        uint16_t* dst2) {
+  constexpr int kNeed = kKind == kCentroid ? kNeedSum : (kNeedMax | kNeedMin);
+  constexpr int C = kNV * 8;
+  const int R = cm.rows_per_tile;
+  const int cv = blk * kWave + lane_id();
+  const bool on = cv < kNV;
+  const uint16_t* tile = cm.x + row * (long long)R * C + (on ? cv : 0) * 8;
+  Acc acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc_init<kNeed>(acc[e]);
+  for (int r0 = 0; r0 < R; r0 += kColRows) {
+    U4 v[kColRows];
+#pragma unroll
+    for (int u = 0; u < kColRows; ++u)
+      v[u] = r0 + u < R ? ld16_stream(tile + (long long)(r0 + u) * C) : U4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < kColRows; ++u) {
+      if (r0 + u < R) {  // uniform (no break: the loads stay in registers)
+        float f[8];
+        unpack8(v[u], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc_add<kNeed>(acc[e], f[e]);
+      }
+    }
+  }
+  if (on) {
+    if constexpr (kKind == kCentroid) {
+      st16(dst + cv * 8, pack_value(acc, VTX_REDUCE_MEAN, R));
+    } else {
+      st16(dst + cv * 8, pack_value(acc, VTX_REDUCE_MAX, R));
+      st16(dst2 + cv * 8, pack_value(acc, VTX_REDUCE_MIN, R));
+    }
+  }
+}
+
+// Tiles of the closed pages reduced as the page-reduce launch for rows of
+// kNV 16-byte vectors would, for kernels whose scoring layout is not the tile
+// layout; wave-level, work units first, first + stride, ...  A unit is a
+// tile for the tile_reduce_vec widths (kNV 8, 16, 32, 64), else a part of 64
+// column vectors of a tile (tile_reduce_colvec_part), so that the waves
+// share a wide tile and each issues its loads in one trip.
+template <int kNV>
+__host__ __device__ constexpr int tile_parts() {
+  return (kNV == 8 || kNV == 16 || kNV == 32 || kNV == 64) ? 1 : (kNV + kWave - 1) / kWave;
+}
+
 template <int kNV, int kLocRegs, int kKind>
 __device__ __forceinline__ void cmean_tiles_any(const CmArgs& cm, const Closing<kLocRegs>& c, int first, int stride) {
-  const int tiles = c.count * cm.heads;
-  for (int t = first; t < tiles; t += stride) {
-    const long long row = (long long)closing_base(c, t / cm.heads) + (t % cm.heads);
+  constexpr int kParts = tile_parts<kNV>();
+  constexpr bool kVecWidth = kNV == 8 || kNV == 16 || kNV == 32 || kNV == 64;
+  const int units = c.count * cm.heads * kParts;
+  for (int t = first; t < units; t += stride) {
+    const int tile = t / kParts;
+    const long long row = (long long)closing_base(c, tile / cm.heads) + (tile % cm.heads);
     if (!tile_in_range(cm, row)) continue;
-    tile_reduce_any<kNV, kKind>(cm, row, cm.out + row * cm.cols, cm.out2 ? cm.out2 + row * cm.cols : nullptr);
+    uint16_t* dst = cm.out + row * cm.cols;
+    uint16_t* dst2 = cm.out2 ? cm.out2 + row * cm.cols : nullptr;
+    if constexpr (kVecWidth) tile_reduce_vec<kNV, kKind>(cm, row, dst, dst2);
+    else tile_reduce_colvec_part<kNV, kKind>(cm, row, t % kParts, dst, dst2);
   }
 }
 
