@@ -156,6 +156,79 @@ __device__ __forceinline__ void query_mean_lds(const FusedArgs& a, const uint16_
   }
 }
 
+// query_mean_lds in two halves, for a mean of one round (G <= 2 *
+// kMeanRowsIn rows, 2 * D / 8 threads at most the workgroup's): issue loads
+// the thread's rows, finish adds them and completes the mean with
+// query_mean_lds's arithmetic in its order (the same bits), so that the
+// caller can issue other loads in between, which then share the round trip.
+struct MeanLoads {
+  vtx::U4 r[kMeanRowsIn];
+};
+
+__device__ __forceinline__ bool query_mean_one_round(const FusedArgs& a) {
+  return a.G <= 2 * kMeanRowsIn && 2 * (a.dim / 8) <= (int)blockDim.x;
+}
+
+// Every thread issues its loads (threads past 2 * D / 8 read column 0 again
+// and do not use it): no branch, so the count of loads in flight is the same
+// on every path and a later wait for these rows waits for nothing issued
+// after them.
+__device__ __forceinline__ void query_mean_issue(const FusedArgs& a, const uint16_t* qb, MeanLoads& ml) {
+  const int D = a.dim;
+  const int nv = D / 8;
+  const int t = (int)threadIdx.x;
+  const bool on = t < 2 * nv;
+  const int h = on && t >= nv ? 1 : 0;
+  const int c = on ? t - h * nv : 0;
+#pragma unroll
+  for (int j = 0; j < kMeanRowsIn; ++j) {
+    const int g = 4 * (j / 2) + 2 * h + j % 2;
+    ml.r[j] = vtx::ld16(qb + (long long)(g < a.G ? g : a.G - 1) * D + c * 8);
+  }
+}
+
+__device__ __forceinline__ void query_mean_finish(const FusedArgs& a, const MeanLoads& ml, int row, bool store,
+                                                  uint16_t* qm, float (*part)[kMeanPartStride]) {
+  const int D = a.dim;
+  const int nv = D / 8;
+  const int t = (int)threadIdx.x;
+  const bool on = t < 2 * nv;
+  const int h = on && t >= nv ? 1 : 0;
+  const int c = on ? t - h * nv : 0;
+  // (added in every thread, so that no use of the loads sits in a branch the
+  // compiler could move them into)
+  float acc[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMeanRowsIn; ++j) {
+    const bool in = 4 * (j / 2) + 2 * h + j % 2 < a.G;
+    float f[8];
+    vtx::unpack8(ml.r[j], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j % 2][e] = in ? acc[j % 2][e] + f[e] : acc[j % 2][e];
+  }
+  if (on && h == 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      part[c][e] = acc[0][e];
+      part[c][8 + e] = acc[1][e];
+    }
+  }
+  __syncthreads();
+  if (on && h == 0) {
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      b[e] = vtx::f32_to_bf16((((acc[0][e] + acc[1][e]) + part[c][e]) + part[c][8 + e]) * a.inv_g);
+    const vtx::U4 m{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+    vtx::st16(qm + c * 8, m);
+    if (store && a.x_out) vtx::st16(a.x_out + (long long)row * D + c * 8, m);
+  }
+}
+
 // Query row of segment `seg` for this lane's columns: the bf16-rounded
 // fp32 mean of its G rows (torch's mean), or the row itself when G == 0.
 // Lanes with `store` set (one lane group per row) also write the mean to x_out.
@@ -654,15 +727,16 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
                                                        (int)gridDim.x * kWaves);
     }
   };
-  float xs[VPL][8];
+  vtx::U4 xq[VPL];  // the query mean as packed bf16 pairs (what the dot steps take)
   vtx::U4 qv[kQRegs][VPL];
   if (w >= chunk_items) {  // query rows past the segments: only their mean
     build_closing();
     const long long row = segments + (w - chunk_items);
     if (a.x_out && a.G > 0 && row < a.q_rows) {
-      if (a.G <= kQRegs)
+      if (a.G <= kQRegs) {
+        float xs[VPL][8];
         query_row<LPR, VPL, kQRegs>(a, qv, false, a.q + row * a.G * D, (int)row, wave == 0 && grp == 0, col, xs);
-      else
+      } else
         query_mean_lds(a, a.q + row * a.G * D, (int)row, true, qm_row, qm_part);
     }
     cm_tiles();
@@ -700,8 +774,12 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   const bool mean_in_lds = a.G > kQRegs;
   if (c >= workers) {  // nothing to score (or an inactive segment): only the mean
     if (c == 0 && a.x_out) {
-      if (mean_in_lds) query_mean_lds(a, qb, seg, true, qm_row, qm_part);
-      else query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+      if (mean_in_lds) {
+        query_mean_lds(a, qb, seg, true, qm_row, qm_part);
+      } else {
+        float xs[VPL][8];
+        query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+      }
     }
     cm_tiles();
     return;
@@ -716,13 +794,15 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   const bool tail_bitonic = k <= vtx::kMaxBitonicRunK && n <= a.row_cap && n <= (long long)T * kRunR;
   if (!tail_bitonic) vtx::select_init<T>(sel, k, sh);
   const int32_t* dseg = a.didx + start;
-  if (mean_in_lds) {  // workgroup-uniform
-    query_mean_lds(a, qb, seg, c == 0, qm_row, qm_part);
-    __syncthreads();
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) vtx::unpack8(vtx::ld16(qm_row + (v * LPR + col) * 8), xs[v]);
-  }
-
+  // this wave's positions of chunk ch: [p0, p0 + cnt), none when cnt <= 0
+  auto wave_share = [&](long long ch, long long& p0, int& cnt) {
+    const long long c0 = ch * kChunk;
+    const long long cn = min((long long)kChunk, n - c0);
+    long long share = (cn + kWaves - 1) / kWaves;
+    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
+    p0 = c0 + (long long)wave * share;
+    cnt = p0 < c0 + cn ? (int)min(share, c0 + cn - p0) : 0;
+  };
   // ---- scores of this workgroup's chunks
   // Staged pre-selection: when every workgroup of the segment scores one
   // chunk, k <= 64 and the segment has at most kStageLists chunks, each
@@ -738,22 +818,8 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
   int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);  // row ids by position (row_cap entries)
   uint32_t hcomp = 0;  // hier: this lane's composite and its row id
   int hrid = 0;
-  bool have_mean = mean_in_lds;
-  for (long long ch = c; ch < nchunks; ch += cps) {
-    const long long c0 = ch * kChunk;
-    const long long cn = min((long long)kChunk, n - c0);
-    long long share = (cn + kWaves - 1) / kWaves;
-    share = (share + kRowsPerLoad - 1) / kRowsPerLoad * kRowsPerLoad;
-    const long long p0 = c0 + (long long)wave * share;
-    if (p0 >= c0 + cn) continue;  // wave-uniform
-    const int cnt = (int)min(share, c0 + cn - p0);
-    const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
-    if (!have_mean) {
-      query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
-      have_mean = true;
-    }
-    int r;
-    float sc = vtx::score_pass<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xs, grp, col, &r);
+  // a scored pass at positions p0 + ...: this lane's score sc, at position r
+  auto pass_done = [&](long long p0, int my_row, int r, float sc) {
     if constexpr (cm_on) {
       if (n_close > 0) {  // uniform
         // pages whose centroid this launch's CMean rewrites: scored against
@@ -766,7 +832,7 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
           vtx::U4 cen[VPL];
           vtx::fresh_centroid_rows<LPR, VPL>(cma, __builtin_amdgcn_readlane(my_rid, l),
                                              fresh_row + wave * kMaxQueryDim, grp, col, cen);
-          const float f = vtx::score_vec_rows<LPR, VPL>(cen, xs);
+          const float f = vtx::score_vec_rows_packed<LPR, VPL>(cen, xq);
           if (lane == l) sc = f;
         }
       }
@@ -780,6 +846,73 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
       hrid = __shfl(my_row, r < 0 ? 0 : r, vtx::kWave);
       hcomp = vtx::bitonic_comp(r >= 0, vtx::score_key(sb), (int)(p0 + r));
     }
+  };
+  // chunks ch0, ch0 + cps, ... with the query mean in xq (have_mean), or
+  // formed from qv / qb at the first pass
+  auto score_chunks = [&](long long ch0, bool have_mean) {
+    for (long long ch = ch0; ch < nchunks; ch += cps) {
+      long long p0;
+      int cnt;
+      wave_share(ch, p0, cnt);
+      if (cnt <= 0) continue;  // wave-uniform
+      const int my_row = lane < cnt ? dseg[p0 + lane] : -1;
+      if (!have_mean) {
+        float xs[VPL][8];
+        query_row<LPR, VPL, kQRegs>(a, qv, q_in_regs, qb, seg, store_mean, col, xs);
+        vtx::pack_query<VPL>(xs, xq);
+        have_mean = true;
+      }
+      int r;
+      const float sc = vtx::score_pass_packed<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, cnt, xq, grp, col, &r);
+      pass_done(p0, my_row, r, sc);
+    }
+  };
+  // the mean formed in LDS, read as packed pairs
+  auto load_xq = [&]() {
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) xq[v] = vtx::ld16(qm_row + (v * LPR + col) * 8);
+  };
+  auto score_all = [&]() {
+    if (mean_in_lds) {  // workgroup-uniform
+      query_mean_lds(a, qb, seg, c == 0, qm_row, qm_part);
+      __syncthreads();
+      load_xq();
+    }
+    score_chunks(c, mean_in_lds);
+  };
+  // Wide rows and a mean of one round: the query rows and the first chunk's
+  // row ids are requested together, the first chunk's rows right after the
+  // row ids, and the mean is formed while the rows are in flight (the query
+  // loads, issued first, are back before the row loads).  The raw query rows
+  // are not held in registers on this path.
+  if constexpr (VPL > 2) {
+    if (mean_in_lds && query_mean_one_round(a)) {  // uniform
+      MeanLoads ml;
+      query_mean_issue(a, qb, ml);
+      __builtin_amdgcn_sched_barrier(0);  // the query loads stay ahead of the row loads
+      long long p0;
+      int cnt;
+      wave_share(c, p0, cnt);
+      // (loaded unconditionally, as the query rows: a wave without pages in
+      // the chunk reads position 0's row id and pool row 0 and uses neither)
+      const int rid = dseg[lane < cnt ? p0 + lane : 0];
+      const int my_row = lane < cnt ? rid : -1;
+      vtx::RowLoads<LPR, VPL, kPass> rl;
+      vtx::row_issue<LPR, VPL, kPass>(a.y, a.y_rows, a.dim, my_row, grp, col, rl);
+      query_mean_finish(a, ml, seg, c == 0, qm_row, qm_part);
+      __syncthreads();
+      load_xq();
+      if (cnt > 0) {  // uniform
+        int r;
+        const float sc = vtx::row_score<LPR, VPL, kPass>(rl, xq, cnt, grp, col, &r);
+        pass_done(p0, my_row, r, sc);
+      }
+      score_chunks(c + cps, true);
+    } else {
+      score_all();
+    }
+  } else {
+    score_all();
   }
   // (wave 0 of chunk 0 always has pages, so the mean has been stored)
   if (hier && c < workers) {  // uniform: this chunk's best k, staged as list c of the segment

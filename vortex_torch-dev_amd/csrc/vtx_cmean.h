@@ -325,6 +325,15 @@ __device__ __forceinline__ float score_vec_rows(const U4 (&cen)[VPL], const floa
   return f;
 }
 
+// score_vec_rows with the query slice as packed bf16 pairs (the same bits).
+template <int LPR, int VPL>
+__device__ __forceinline__ float score_vec_rows_packed(const U4 (&cen)[VPL], const U4 (&xq)[VPL]) {
+  float f = dot_row_packed<VPL>(cen, xq);
+#pragma unroll
+  for (int d = LPR / 2; d >= 1; d >>= 1) f += xshfl(f, d);
+  return f;
+}
+
 // Whether the lane's pass position (r >= 0, row my_rid) is a tile the
 // in-kernel CMean writes: a row in [page * H, page * H + H) of a closed page,
 // inside the pool and the centroid pool.

@@ -209,4 +209,29 @@ __device__ __forceinline__ float dot_row(const U4 (&w)[VPL], const float (&xs)[V
   return s;
 }
 
+// The query slice xs (bf16 values) as the packed bf16 pairs dot_row feeds
+// its steps (exact).
+template <int VPL>
+__device__ __forceinline__ void pack_query(const float (&xs)[VPL][8], U4 (&xq)[VPL]) {
+#pragma unroll
+  for (int v = 0; v < VPL; ++v)
+    xq[v] = U4{pack_bf16x2(xs[v][0], xs[v][1]), pack_bf16x2(xs[v][2], xs[v][3]), pack_bf16x2(xs[v][4], xs[v][5]),
+               pack_bf16x2(xs[v][6], xs[v][7])};
+}
+
+// dot_row with the query slice as packed bf16 pairs (xq[v] holds the bits
+// pack_bf16x2 makes of xs[v]): the same steps, the same bits.
+template <int VPL>
+__device__ __forceinline__ float dot_row_packed(const U4 (&w)[VPL], const U4 (&xq)[VPL]) {
+  float s = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    s = dot2_bf16(w[v].x, xq[v].x, s);
+    s = dot2_bf16(w[v].y, xq[v].y, s);
+    s = dot2_bf16(w[v].z, xq[v].z, s);
+    s = dot2_bf16(w[v].w, xq[v].w, s);
+  }
+  return s;
+}
+
 }  // namespace vtx

@@ -91,6 +91,70 @@ __device__ __forceinline__ void row_pass(const uint16_t* const (&ys)[kRows], lon
   *r = ((col % kShare) == 0 && pos < cnt) ? pos : -1;
 }
 
+// The two halves of a one-pool, one-query pass whose slots load in one
+// batch (row_pass with kRows = kG = 1 and every slot in flight together), so
+// that other loads and arithmetic can sit between the loads and their use:
+// row_issue issues the pass's row loads into a RowLoads, row_score consumes
+// them with row_pass's arithmetic (the same partials, the same
+// reduce-scatter), so the scores carry the same bits.
+template <int LPR, int VPL, int kPass>
+struct RowLoads {
+  static constexpr int kSlots = kPass / (kWave / LPR);
+  U4 buf[kSlots][VPL];
+  bool live[kSlots];
+};
+
+template <int LPR, int VPL, int kPass>
+__device__ __forceinline__ void row_issue(const uint16_t* y, long long y_rows, int D, int my_row, int grp, int col,
+                                          RowLoads<LPR, VPL, kPass>& rl) {
+  constexpr int kRowsPerLoad = kWave / LPR;
+  constexpr int kSlots = RowLoads<LPR, VPL, kPass>::kSlots;
+  static_assert(kSlots >= 1 && kSlots <= LPR && kSlots * kRowsPerLoad == kPass, "pass geometry");
+  int first = __builtin_amdgcn_readlane(my_row, 0);
+  if (first < 0 || first >= y_rows) first = 0;
+  // Every slot is loaded (a slot past the pass reads row `first` again and
+  // is not live): no branch, so no value waits for its load here.
+#pragma unroll
+  for (int ii = 0; ii < kSlots; ++ii) {
+    const int row = __shfl(my_row, ii * kRowsPerLoad + grp, kWave);
+    rl.live[ii] = row >= 0 && row < y_rows;
+    const long long off = (long long)(rl.live[ii] ? row : first) * D;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) rl.buf[ii][v] = ld16_stream(y + off + (v * LPR + col) * 8);
+  }
+}
+
+// (the query slice as packed bf16 pairs, dot_row_packed: the bits of
+// dot_row's partials)
+template <int LPR, int VPL, int kPass>
+__device__ __forceinline__ float row_score(const RowLoads<LPR, VPL, kPass>& rl, const U4 (&xq)[VPL], int cnt, int grp,
+                                           int col, int* r) {
+  constexpr int kRowsPerLoad = kWave / LPR;
+  constexpr int kSlots = RowLoads<LPR, VPL, kPass>::kSlots;
+  float acc[kSlots];
+#pragma unroll
+  for (int ii = 0; ii < kSlots; ++ii) {
+    const float s = dot_row_packed<VPL>(rl.buf[ii], xq);
+    acc[ii] = rl.live[ii] ? s : 0.f;
+  }
+#pragma unroll
+  for (int half = kSlots / 2, stride = LPR / 2; half >= 1; half >>= 1, stride >>= 1) {
+    const bool upper = (col & stride) != 0;
+#pragma unroll
+    for (int t = 0; t < half; ++t) {
+      const float send = upper ? acc[t] : acc[t + half];
+      const float keep = upper ? acc[t + half] : acc[t];
+      acc[t] = keep + xshfl(send, stride);
+    }
+  }
+  constexpr int kShare = LPR / kSlots;
+#pragma unroll
+  for (int d = kShare / 2; d >= 1; d >>= 1) acc[0] += xshfl(acc[0], d);
+  const int pos = (col / kShare) * kRowsPerLoad + grp;
+  *r = ((col % kShare) == 0 && pos < cnt) ? pos : -1;
+  return acc[0];
+}
+
 // Dot products of kG fp32 query rows with one gathered row per position:
 // the lane's partial is the vtx::dot_row chain over its columns.
 template <int LPR, int VPL, int kPass, int kG>
@@ -129,6 +193,18 @@ __device__ __forceinline__ void quest_pass_multi(const uint16_t* ymax, const uin
                                      }
                                      return s;
                                    });
+}
+
+// score_pass with the query slice as packed bf16 pairs (dot_row_packed:
+// the same partials, the same bits).
+template <int LPR, int VPL, int kPass>
+__device__ __forceinline__ float score_pass_packed(const uint16_t* y, long long y_rows, int D, int my_row, int cnt,
+                                                   const U4 (&xq)[VPL], int grp, int col, int* r) {
+  const uint16_t* const ys[1] = {y};
+  float sc[1];
+  row_pass<LPR, VPL, kPass, 1, 1>(ys, y_rows, D, my_row, cnt, grp, col, r, sc,
+                                  [&](const U4 (&rows)[1][VPL], int) { return dot_row_packed<VPL>(rows[0], xq); });
+  return sc[0];
 }
 
 // Single-query form: returns the lane's finished score.
