@@ -718,12 +718,21 @@ __global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr
       n_close = closing.count;
     }
   };
-  // this work id's share of the CMean tiles (after its scores are counted in)
+  // this work id's share of the CMean tiles (after its scores are counted
+  // in), by rank: the work id itself, or for wide rows (D >= 512, the large
+  // chunks: segments of uneven length leave many slots idle) the highest
+  // chunk slots first, slot cps - 1 of every segment, then cps - 2, ...:
+  // slots past a segment's chunks only average the query and end at once, so
+  // the tiles stay off the selecting workgroups' path (rank of work id
+  // w = (seg, c): (cps - 1 - c) * segments + seg; work ids past the slots
+  // keep their own number).  Measured: C5 12.9 -> 12.7 us per launch; at C3,
+  // where every slot works, the same order was 2 us slower than the work id.
+  const long long trank = VPL > 2 && w < chunk_items ? (long long)(cps - 1 - w % cps) * segments + w / cps : w;
   auto cm_tiles = [&]() {
     if constexpr (cm_on) {
-      // uniform: units (tiles, or parts of wide tiles) w * waves + wave, + grid * waves, ...
-      if (w * kWaves < (long long)n_close * cma.heads * vtx::tile_parts<LPR * VPL>())
-        vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(cma, closing, (int)(w * kWaves) + wave,
+      // uniform: units (tiles, or parts of wide tiles) trank * waves + wave, + grid * waves, ...
+      if (trank * kWaves < (long long)n_close * cma.heads * vtx::tile_parts<LPR * VPL>())
+        vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(cma, closing, (int)(trank * kWaves) + wave,
                                                        (int)gridDim.x * kWaves);
     }
   };
