@@ -673,9 +673,12 @@ __device__ __forceinline__ void merge_staged(const uint64_t* lists, int workers,
 // As in indexer_fused_kernel, the operands of the first loads (the block
 // tables' bounds, loc and the sizes the work id needs, gridDim.x / 8
 // included: the grid size is itself a kernel argument) lead the argument
-// list, so that they are preloaded into SGPRs.
+// list, so that they are preloaded into SGPRs.  Rows of one vector per lane
+// ask for four waves per SIMD (at most 128 VGPRs), so that 16 waves of
+// split workgroups fit a CU, as the host's chunk sizing assumes.
 template <int T, int LPR, int VPL, int kPass, int kCmRegs>
-__global__ __launch_bounds__(T) void indexer_split_kernel(const int32_t* dindptr, const int32_t* sindptr,
+__global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(const int32_t* dindptr,
+                                                                              const int32_t* sindptr,
                                                           const int64_t* loc, int32_t segments, int32_t loc_n,
                                                           int32_t cps, int32_t per_xcd, FusedArgs a,
                                                           int32_t* counters, vtx::CmArgs cma) {
@@ -1118,21 +1121,30 @@ int launch_dim(const FusedArgs& a, const vtx::CmArgs* cm, int blocks, size_t lds
   return vtx::check_launch("indexer_fused");
 }
 
-// Threads per split workgroup: 512 for rows of up to two vectors per lane
-// (the selecting workgroup then holds at most four of a 2046-page segment's
-// scores per thread: C3 17.2 us per launch against 20.9 us with 256 threads
-// and 18.3 with 1024), 256 for wider rows (two workgroups per CU fit their
-// registers; 512 threads measured 0.5 us slower at C5).
-int split_threads(int dim) { return dim <= 256 ? 512 : 256; }
-
-// Pages per wave pass of the split layout (small chunks; large ones are
-// twice this) and pages per split workgroup.
-int split_pass(int dim) { return dim <= 128 ? 32 : 16; }
-int split_chunk(int dim, bool large) { return (split_threads(dim) / 64) * split_pass(dim) * (large ? 2 : 1); }
+// Threads per split workgroup and pages per wave pass, for small chunks and
+// large ones (twice the pages per workgroup), by head dim:
+//   D = 64, 128, 256: 512 threads x 32 / 32 / 16 pages, large twice the pass
+//            (rows of up to two vectors per lane; unstaged, 512 threads let
+//            the selecting workgroup hold at most four of a 2046-page
+//            segment's scores per thread: C3 17.2 us against 20.9 with 256);
+//   D = 128 with the staged pre-selection (`quad`): small chunks of the same
+//            256 pages as 256 threads x 64 (four waves, one score per lane:
+//            the chunk's select merges four full lists in two rounds instead
+//            of eight half-full ones in three; C3 15.2 -> 14.7 us per launch);
+//   D >= 512: 256 threads x 16 pages, large 32 (two workgroups per CU fit
+//            their registers; 512 threads measured 0.5 us slower at C5).
+int split_threads(int dim, bool large, bool quad) { return dim <= 256 && !(quad && !large) ? 512 : 256; }
+int split_pass(int dim, bool large, bool quad) {
+  if (quad && !large) return 64;
+  return (dim <= 128 ? 32 : 16) * (large ? 2 : 1);
+}
+int split_chunk(int dim, bool large, bool quad) {
+  return (split_threads(dim, large, quad) / 64) * split_pass(dim, large, quad);
+}
 
 template <int P, int kCm>
 int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
-                    const vtx::CmArgs& cm) {
+                    const vtx::CmArgs& cm, bool quad) {
   const int32_t nnz = (int32_t)cm.nnz;  // at most vtx::kCmLoc with the CMean, else 0
   const int32_t xcd = blocks / 8;       // work ids per XCD (blocks is a multiple of 8)
   switch (a.dim) {
@@ -1140,9 +1152,13 @@ int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, 
       indexer_split_kernel<512, 8, 1, 2 * P, kCm>
           <<<blocks, 512, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
       break;
-    case 128:
-      indexer_split_kernel<512, 16, 1, 2 * P, kCm>
-          <<<blocks, 512, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+    case 128:  // (P = 16: small chunks, 32: large; quad: split_threads, split_pass)
+      if (P == 16 && quad)
+        indexer_split_kernel<256, 16, 1, 64, kCm>
+            <<<blocks, 256, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
+      else
+        indexer_split_kernel<512, 16, 1, 2 * P, kCm>
+            <<<blocks, 512, lds, s>>>(a.dindptr, a.sindptr, cm.loc, a.segments, nnz, cps, xcd, a, counters, cm);
       break;
     case 256:
       indexer_split_kernel<512, 16, 2, P, kCm>
@@ -1163,15 +1179,15 @@ int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, 
 
 template <int P>
 int launch_split_pass(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
-                      const vtx::CmArgs* cm) {
-  if (cm) return launch_split_cm<P, vtx::kCmLoc / vtx::kWave>(a, counters, cps, blocks, lds, s, *cm);
-  return launch_split_cm<P, 0>(a, counters, cps, blocks, lds, s, vtx::CmArgs{});
+                      const vtx::CmArgs* cm, bool quad) {
+  if (cm) return launch_split_cm<P, vtx::kCmLoc / vtx::kWave>(a, counters, cps, blocks, lds, s, *cm, quad);
+  return launch_split_cm<P, 0>(a, counters, cps, blocks, lds, s, vtx::CmArgs{}, quad);
 }
 
-int launch_split(const FusedArgs& a, int32_t* counters, int cps, bool large, int blocks, size_t lds,
+int launch_split(const FusedArgs& a, int32_t* counters, int cps, bool large, bool quad, int blocks, size_t lds,
                  hipStream_t s, const vtx::CmArgs* cm) {
-  return large ? launch_split_pass<32>(a, counters, cps, blocks, lds, s, cm)
-               : launch_split_pass<16>(a, counters, cps, blocks, lds, s, cm);
+  return large ? launch_split_pass<32>(a, counters, cps, blocks, lds, s, cm, quad)
+               : launch_split_pass<16>(a, counters, cps, blocks, lds, s, cm, quad);
 }
 
 }  // namespace
@@ -1363,10 +1379,18 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     // serves twice the pages, and a segment hands over half as many lists
     // (C5: 13.7 -> 12.8 us per launch; at C3 the large chunks are slower).
     const long long mid = want - reserved_bos - reserved_eos > 1 ? want - reserved_bos - reserved_eos : 1;
-    const long long resident = (1024LL / split_threads(head_dim)) * cus;  // split workgroups resident at once
-    const long long small = split_chunk(head_dim, false);
-    const bool large = head_dim >= 512 || (long long)eff_batch_size * ((mid + small - 1) / small) > resident;
-    const int chunk = split_chunk(head_dim, large);
+    // (split workgroups resident at once: 16 waves per CU)
+    const long long small = split_chunk(head_dim, false, false);
+    const long long small_chunks = (mid + small - 1) / small;
+    // four-wave workgroups at D = 128 when every chunk of every segment is
+    // one workgroup's and the chunks stage their lists
+    const bool quad = head_dim == 128 && zone != nullptr && a.topk <= vtx::kMaxBitonicRunK &&
+                      eff_batch_size <= kStageMaxSegments && small_chunks <= kStageLists &&
+                      (long long)eff_batch_size * small_chunks <= (1024LL / 256) * cus;
+    const bool large = head_dim >= 512 ||
+                       (long long)eff_batch_size * small_chunks > (1024LL / split_threads(head_dim, false, quad)) * cus;
+    const long long resident = (1024LL / split_threads(head_dim, large, quad)) * cus;
+    const int chunk = split_chunk(head_dim, large, quad);
     long long cps = (mid + chunk - 1) / chunk;
     const long long fill = eff_batch_size > 0 ? resident / eff_batch_size : 1;
     if (cps > fill) cps = fill;
@@ -1383,7 +1407,7 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
     if (items == 0) return VTX_OK;
     a.stage = zone;  // the staged pre-selection's lists (segments past kStageMaxSegments do not stage)
-    return launch_split(a, seg_counters, (int)cps, large, (int)items, lds, s, cmp);
+    return launch_split(a, seg_counters, (int)cps, large, quad, (int)items, lds, s, cmp);
   }
 
   // the planner's schedule, when it covers this launch's segments
