@@ -33,6 +33,8 @@
 // dot product (vtx::dot_row) and the reduce-scatter tree over the LPR lanes
 // are the ones gemv.hip uses, so the scores are bit-identical to the GeMV
 // kernel's for the same query.
+#include <algorithm>
+
 #include "vtx_device.h"
 #include "vtx_fused_schedule.h"
 #include "vtx_host.h"
@@ -707,10 +709,12 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
 
   long long cm_pos[kLocRegs];
   if constexpr (cm_on) vtx::closing_load(loc, loc_n, cm_pos);
-  // per_xcd = gridDim.x / 8 (the host rounds the grid to a multiple of 8),
-  // passed so that the work id waits for no kernel-argument load
+  // per_xcd = the work ids per XCD (8 * per_xcd workgroups take work ids;
+  // the host rounds them to a multiple of 8), passed so that the work id
+  // waits for no kernel-argument load
   const long long w = (long long)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   const long long chunk_items = (long long)segments * cps;
+  const long long slots = 8LL * per_xcd;
   vtx::Closing<kLocRegs> closing{};
   int n_close = 0;
   // the closed pages of loc (waits for the loc loads: called once the
@@ -721,24 +725,32 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
       n_close = closing.count;
     }
   };
-  // this work id's share of the CMean tiles (after its scores are counted
-  // in), by rank: the work id itself, or for wide rows (D >= 512, the large
-  // chunks: segments of uneven length leave many slots idle) the highest
-  // chunk slots first, slot cps - 1 of every segment, then cps - 2, ...:
-  // slots past a segment's chunks only average the query and end at once, so
-  // the tiles stay off the selecting workgroups' path (rank of work id
-  // w = (seg, c): (cps - 1 - c) * segments + seg; work ids past the slots
-  // keep their own number).  Measured: C5 12.9 -> 12.7 us per launch; at C3,
-  // where every slot works, the same order was 2 us slower than the work id.
-  const long long trank = VPL > 2 && w < chunk_items ? (long long)(cps - 1 - w % cps) * segments + w / cps : w;
+  // The CMean's work units (tiles, or parts of wide tiles).  For wide rows
+  // (D >= 512) the host appends workgroups of their own past the work ids:
+  // they reduce every unit as the launch starts, unit r * waves + wave, +
+  // tile workgroups * waves, ..., so no unit waits behind a segment's select
+  // or delays one (handed to the work ids after their count-in, a unit landed
+  // on a selecting workgroup in some launches and delayed its end by 1-2 us
+  // at C5).  Narrower rows (and a grid without them) share the units out
+  // over the work ids after their count-in: unit w * waves + wave, + grid *
+  // waves, ...
+  constexpr bool kTileGroups = cm_on && VPL > 2;
   auto cm_tiles = [&]() {
     if constexpr (cm_on) {
-      // uniform: units (tiles, or parts of wide tiles) trank * waves + wave, + grid * waves, ...
-      if (trank * kWaves < (long long)n_close * cma.heads * vtx::tile_parts<LPR * VPL>())
-        vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(cma, closing, (int)(trank * kWaves) + wave,
+      const bool shared = !kTileGroups || (long long)gridDim.x == slots;
+      if (shared && w * kWaves < (long long)n_close * cma.heads * vtx::tile_parts<LPR * VPL>())  // uniform
+        vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(cma, closing, (int)(w * kWaves) + wave,
                                                        (int)gridDim.x * kWaves);
     }
   };
+  if constexpr (kTileGroups) {
+    if ((long long)blockIdx.x >= slots) {  // uniform: a CMean tile workgroup
+      build_closing();
+      vtx::cmean_tiles_any<LPR * VPL, kLocRegs, vtx::kCentroid>(
+          cma, closing, (int)(blockIdx.x - slots) * kWaves + wave, (int)(gridDim.x - slots) * kWaves);
+      return;
+    }
+  }
   vtx::U4 xq[VPL];  // the query mean as packed bf16 pairs (what the dot steps take)
   vtx::U4 qv[kQRegs][VPL];
   if (w >= chunk_items) {  // query rows past the segments: only their mean
@@ -1142,11 +1154,12 @@ int split_chunk(int dim, bool large, bool quad) {
   return (split_threads(dim, large, quad) / 64) * split_pass(dim, large, quad);
 }
 
+// blocks: the grid, xcd: work ids per XCD (8 * xcd workgroups take work
+// ids, the rest are CMean tile workgroups)
 template <int P, int kCm>
-int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
-                    const vtx::CmArgs& cm, bool quad) {
+int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, int32_t xcd, size_t lds,
+                    hipStream_t s, const vtx::CmArgs& cm, bool quad) {
   const int32_t nnz = (int32_t)cm.nnz;  // at most vtx::kCmLoc with the CMean, else 0
-  const int32_t xcd = blocks / 8;       // work ids per XCD (blocks is a multiple of 8)
   switch (a.dim) {
     case 64:
       indexer_split_kernel<512, 8, 1, 2 * P, kCm>
@@ -1178,17 +1191,26 @@ int launch_split_cm(const FusedArgs& a, int32_t* counters, int cps, int blocks, 
 }
 
 template <int P>
-int launch_split_pass(const FusedArgs& a, int32_t* counters, int cps, int blocks, size_t lds, hipStream_t s,
-                      const vtx::CmArgs* cm, bool quad) {
-  if (cm) return launch_split_cm<P, vtx::kCmLoc / vtx::kWave>(a, counters, cps, blocks, lds, s, *cm, quad);
-  return launch_split_cm<P, 0>(a, counters, cps, blocks, lds, s, vtx::CmArgs{}, quad);
+int launch_split_pass(const FusedArgs& a, int32_t* counters, int cps, int blocks, int32_t xcd, size_t lds,
+                      hipStream_t s, const vtx::CmArgs* cm, bool quad) {
+  if (cm) return launch_split_cm<P, vtx::kCmLoc / vtx::kWave>(a, counters, cps, blocks, xcd, lds, s, *cm, quad);
+  return launch_split_cm<P, 0>(a, counters, cps, blocks, xcd, lds, s, vtx::CmArgs{}, quad);
 }
 
-int launch_split(const FusedArgs& a, int32_t* counters, int cps, bool large, bool quad, int blocks, size_t lds,
-                 hipStream_t s, const vtx::CmArgs* cm) {
-  return large ? launch_split_pass<32>(a, counters, cps, blocks, lds, s, cm, quad)
-               : launch_split_pass<16>(a, counters, cps, blocks, lds, s, cm, quad);
+int launch_split(const FusedArgs& a, int32_t* counters, int cps, bool large, bool quad, int blocks, int32_t xcd,
+                 size_t lds, hipStream_t s, const vtx::CmArgs* cm) {
+  return large ? launch_split_pass<32>(a, counters, cps, blocks, xcd, lds, s, cm, quad)
+               : launch_split_pass<16>(a, counters, cps, blocks, xcd, lds, s, cm, quad);
 }
+
+// Work units of the in-launch CMean per closed (page, head) tile: parts of
+// 64 column vectors for row widths other than 8, 16, 32 or 64 vectors
+// (vtx::tile_parts for the kernel's width).
+int cmean_tile_parts(int head_dim) {
+  const int nv = head_dim / 8;
+  return (nv == 8 || nv == 16 || nv == 32 || nv == 64) ? 1 : (nv + vtx::kWave - 1) / vtx::kWave;
+}
+constexpr long long kMaxTileWorkgroups = 64;  // CMean tile workgroups a split launch appends at most
 
 }  // namespace
 
@@ -1404,10 +1426,22 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
     const size_t lds = (size_t)vtx::sel_slots(a.topk) * 8 + (size_t)a.topk * 4 + (size_t)cap * 6;
     long long items = (long long)eff_batch_size * cps + (a.x_out ? q_rows - eff_batch_size : 0);
     items = (items + 7) / 8 * 8;  // work ids are laid out per XCD
-    if (items > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
     if (items == 0) return VTX_OK;
+    // the in-launch CMean's own workgroups, for wide rows: enough for one
+    // unit per wave if every loc entry closed a page (a loc entry closes at
+    // most one).  Narrower rows share the units out over the work ids after
+    // their count-in (measured: C5 12.73 -> 12.59 us per launch with tile
+    // workgroups; C3 14.44 -> 14.53, so not there)
+    long long tile_wgs = 0;
+    if (cmp && head_dim >= 512) {
+      const long long waves = split_threads(head_dim, large, quad) / vtx::kWave;
+      const long long units = cma.nnz * cma.heads * cmean_tile_parts(head_dim);
+      tile_wgs = std::min((units + waves - 1) / waves, kMaxTileWorkgroups);
+    }
+    if (items + tile_wgs > 0x7fffffffLL) return vtx::fail(VTX_E_INVALID, "indexer_fused: too many workgroups");
     a.stage = zone;  // the staged pre-selection's lists (segments past kStageMaxSegments do not stage)
-    return launch_split(a, seg_counters, (int)cps, large, quad, (int)items, lds, s, cmp);
+    return launch_split(a, seg_counters, (int)cps, large, quad, (int)(items + tile_wgs), (int32_t)(items / 8), lds,
+                        s, cmp);
   }
 
   // the planner's schedule, when it covers this launch's segments
