@@ -811,12 +811,8 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   uint64_t* sel = reinterpret_cast<uint64_t*>(smem);
   int32_t* sel_pay = reinterpret_cast<int32_t*>(smem + (size_t)vtx::sel_slots(k) * sizeof(uint64_t));
   uint16_t* keys = reinterpret_cast<uint16_t*>(sel_pay + k);
-  // the histograms of the final selection (the radix selects) are cleared
-  // now, off its path (the barriers of the arrival order this before the
-  // counting); the bitonic selects of the tail use none
   constexpr int kRunR = 4;  // scores per thread of the tail's bitonic select
   const bool tail_bitonic = k <= vtx::kMaxBitonicRunK && n <= a.row_cap && n <= (long long)T * kRunR;
-  if (!tail_bitonic) vtx::select_init<T>(sel, k, sh);
   const int32_t* dseg = a.didx + start;
   // this wave's positions of chunk ch: [p0, p0 + cnt), none when cnt <= 0
   auto wave_share = [&](long long ch, long long& p0, int& cnt) {
@@ -839,6 +835,10 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   // ends), only the lists are written through for the hand-off.
   const bool hier = a.stage != nullptr && seg < kStageMaxSegments && k <= vtx::kMaxBitonicRunK &&
                     nchunks <= cps && workers <= kStageLists && n <= a.row_cap && n <= 0xffff;  // uniform
+  // the histograms of the final selection (the radix selects) are cleared
+  // now, off its path (the barriers of the arrival order this before the
+  // counting); the staged merge and the tail's bitonic select use none
+  if (!tail_bitonic && !hier) vtx::select_init<T>(sel, k, sh);
   int32_t* rid_lds = reinterpret_cast<int32_t*>(keys + a.row_cap);  // row ids by position (row_cap entries)
   uint32_t hcomp = 0;  // hier: this lane's composite and its row id
   int hrid = 0;
