@@ -159,13 +159,23 @@ def fused_kernel_name(batch: W.DecodeBatch) -> str:
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     layout = fused_layout()
     if layout == 2 or (layout == 0 and segments < 2 * cus):
-        small_pass = 32 if batch.head_dim <= 128 else 16
+        # the library's split_threads / split_pass / chunk choice, with the
+        # topK op's workspace (staging zone present)
+        D = batch.head_dim
+        small_pass = 32 if D <= 128 else 16
+        waves_small = 8 if D <= 256 else 4
         mid = max(1, batch.max_pages_per_request - batch.bos - batch.eos)
-        waves = 8 if batch.head_dim <= 256 else 4
-        large = segments * -(-mid // (waves * small_pass)) > (16 // waves) * cus
+        small_chunks = -(-mid // (waves_small * small_pass))
+        quad = (D == 128 and batch.topk <= 64 and segments <= 512 and small_chunks <= 16
+                and segments * small_chunks <= 4 * cus)
+        threads_small = 256 if quad else 64 * waves_small
+        large = D >= 512 or segments * small_chunks > (1024 // threads_small) * cus
         cm = 4 if batch.batch <= 256 else 0  # the decode CMean in the launch (loc in four registers per lane)
-        T = 512 if batch.head_dim <= 256 else 256
-        return f"indexer_split_kernel<{T}, {lpr}, {vpl}, {small_pass * (2 if large else 1)}, {cm}>"
+        if quad and not large:
+            T, kpass = 256, 64
+        else:
+            T, kpass = (512 if D <= 256 else 256), small_pass * (2 if large else 1)
+        return f"indexer_split_kernel<{T}, {lpr}, {vpl}, {kpass}, {cm}>"
     mp = batch.max_pages_per_request
     T = 256 if mp <= 256 else (512 if mp <= 1024 else 1024)
     # the decode CMean (loc: one token per request) runs in the same launch
