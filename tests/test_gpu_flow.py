@@ -113,7 +113,7 @@ def test_fused_query_mean_is_torch_mean(gpu, G, D, mode):
 
 
 @pytest.mark.parametrize("cmean", [False, True])
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "eos0", "d64", "d256", "d576", "r3", "r9"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c5", "eos0", "d64", "d256", "d576", "d576many", "r3", "r9"])
 def test_fused_segment_and_split_layouts_agree(gpu, name, cmean):
     """FUSED_SEGMENT and FUSED_SPLIT write the same bits: q-mean, scores,
     block table and (with the layer's CMean) centroids."""

@@ -290,6 +290,14 @@ def cmean_case(name: str):
         b = make_batch([4096, 5000, 2048, 3072], pool_pages=1200, seed=26, num_kv_heads=1, group_size=16,
                        head_dim=576, topk=32, bos=1, eos=0)
         return b, decode_loc(b)
+    if name == "d576many":  # MLA rows, 256 loc entries each closing a different page (scored ones
+        # among them): more CMean work units than the split launch's tile workgroups have waves
+        b = make_batch([4096, 5000, 2048, 3072], pool_pages=1200, seed=27, num_kv_heads=1, group_size=16,
+                       head_dim=576, topk=32, bos=1, eos=0)
+        g = torch.Generator().manual_seed(9)
+        pages = torch.cat([torch.as_tensor(p, dtype=torch.int64) for p in b.pages])
+        pick = pages[torch.randperm(pages.numel(), generator=g)[:256]]
+        return b, pick * b.page_size + b.page_size - 1
     if name == "d256":  # wider rows
         b = make_batch([2000, 3000], pool_pages=400, seed=25, head_dim=256, eos=0)
         return b, decode_loc(b)
