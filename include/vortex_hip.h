@@ -209,7 +209,8 @@ int vtx_topk_select(const uint16_t* score, int64_t score_len,
  * S segments: it also holds, at its end, the staging zone in which each
  * workgroup of a segment split over at most 16 of them pre-selects its
  * chunk's best k (k <= 64), so that the last one only merges the lists; the
- * zone needs no initial value, and the counters are the entries before it.
+ * zone, like the counters (the entries before it), is all zero before the
+ * first call, and every call that completes leaves it all zero.
  * A shorter buffer (at least eff_batch_size entries) holds counters only.
  * Calls that share one workspace must be ordered on one stream.  mode: VTX_FUSED_AUTO
  * (split when there are fewer than two segments per compute unit and the
@@ -246,12 +247,12 @@ int64_t vtx_indexer_fused_workspace_len(int32_t segments);
  * the call allocates nothing and takes no workspace.  No counterpart in the
  * reference: it is for callers that cannot allocate (code under graph
  * capture, tight serving loops, harnesses that forbid allocation).  The
- * first call on a device looks the array up and clears its counters (a fill
- * kernel on `stream`, waited for unless the stream is being captured).  At
+ * first call on a device looks the array up and clears it (a fill kernel on
+ * `stream`, waited for unless the stream is being captured).  At
  * most 65,536 segments (eff_batch_size), else VTX_E_INVALID.  Every call on
  * a device shares the array: calls that overlap on one device (other
  * streams, other threads) race and must be serialized by the caller.  A
- * launch that fails (VTX_E_LAUNCH) has the counters cleared again before the
+ * launch that fails (VTX_E_LAUNCH) has the array cleared again before the
  * next call; after a launch that was issued but did not complete (an aborted
  * stream), call vtx_indexer_fused_noalloc_reset.
  */
@@ -266,9 +267,9 @@ int vtx_indexer_fused_noalloc(const uint16_t* q, int64_t q_rows, int32_t group_s
                               int32_t mode, const int32_t* schedule, int64_t schedule_len, void* stream);
 
 /*
- * Clears the arrival counters of vtx_indexer_fused_noalloc's workspace on the
- * current device (a fill kernel on `stream`, waited for unless the stream is
- * being captured).  Allocates nothing.  No counterpart in the reference.
+ * Clears the workspace of vtx_indexer_fused_noalloc (arrival counters and
+ * staging zone) on the current device (a fill kernel on `stream`, waited for
+ * unless the stream is being captured).  Allocates nothing.  No counterpart in the reference.
  */
 int vtx_indexer_fused_noalloc_reset(void* stream);
 

@@ -603,8 +603,10 @@ def test_split_workspace_shared_by_batches_of_several_sizes(gpu):
     """One workspace serves a decode loop whose segment count changes from
     call to call (growing and shrinking, as SGLang's batches do): every call
     equals the same call on a fresh zeroed workspace and on a counters-only
-    buffer (the unstaged path), bit for bit, and leaves every counter the
-    workspace holds at zero."""
+    buffer (the unstaged path), bit for bit, and leaves the whole workspace
+    (counters and staging zone) at zero, so that the MLA calls, whose
+    selecting workgroups read the staged lists as they arrive, never meet a
+    list an earlier call left behind."""
     dev = gpu
     cap = 512
     ws = torch.zeros(_hip.indexer_fused_workspace_len(cap), dtype=torch.int32, device=dev)
@@ -621,6 +623,7 @@ def test_split_workspace_shared_by_batches_of_several_sizes(gpu):
         assert S <= cap
         got = _split_run(batch, case, ws)
         assert int(ws[:cap].abs().sum()) == 0, f"call {i}: counters not back at zero"
+        assert int(ws.abs().sum()) == 0, f"call {i}: staged lists left in the zone"
         fresh = _split_run(batch, case, torch.zeros_like(ws))
         plain = _split_run(batch, case, torch.zeros(S, dtype=torch.int32, device=dev))
         for a, b, c in zip(got, fresh, plain):

@@ -3,12 +3,13 @@ nothing: the split layout's workspace (per-segment arrival counters and the
 staging zone of its pre-selection) lives in a device array of the library
 instead of a caller workspace.
 
-Through the C-ABI (ctypes), two calls in a row — a layout of 64 segments
-split over many workgroups, then a smaller one — each compared bit for bit
-with vtx_indexer_fused given zeroed counters only (so also the staged
+Through the C-ABI (ctypes), calls in a row — a layout of 64 segments split
+over many workgroups, then a smaller one, then MLA rows (whose selecting
+workgroups read the staged lists as they arrive) — each compared bit for
+bit with vtx_indexer_fused given zeroed counters only (so also the staged
 pre-selection against the unstaged path): q-mean, scores and block table.
-A third call repeats the first layout, which only gives the same result if
-the earlier calls left every counter at zero.
+A last call repeats the first layout, which only gives the same result if
+the earlier calls left every counter and staged list place at zero.
 """
 import numpy as np
 import pytest
@@ -56,7 +57,9 @@ def test_noalloc_entry_point_equals_workspace_entry_point(gpu, mode):
     first = (W.c3(), 1)
     second = (W.make_batch([3000, 9000, 700], pool_pages=900, seed=51, num_kv_heads=2, group_size=2,
                            head_dim=128, topk=20, bos=1, eos=1), 2)
-    for batch, seed in (first, second, first):
+    wide = (W.make_batch([5000, 7000, 9000], pool_pages=2000, seed=53, num_kv_heads=1, group_size=16,
+                         head_dim=576, topk=32, bos=1, eos=1), 3)
+    for batch, seed in (first, second, wide, first):
         ic, q, y, S = _case(batch, gpu, seed)
         got = _run(batch, ic, q, y, S, mode, noalloc=True)
         exp = _run(batch, ic, q, y, S, mode, noalloc=False)

@@ -613,41 +613,93 @@ __device__ __forceinline__ V load_coherent(const V* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A device-scope fetch-add of 1 by one lane, its result waited for only
+// where it is used: the address is passed through a VGPR, so the compiler's
+// atomic optimizer (which combines the active lanes' adds into one and
+// waits for its result right away to hand each lane its share) leaves it
+// alone and the round trip overlaps the work that follows.
+__device__ __forceinline__ int fetch_add_one_deferred(int32_t* p) {
+  asm volatile("" : "+v"(p));
+  // (a global-memory pointer again: a flat atomic would also hold up the
+  // next wait for LDS)
+  auto* g = (__attribute__((address_space(1))) int32_t*)p;
+  return __hip_atomic_fetch_add(g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Histogram copies of the split layout's selection (vtx::SelectShared).
 constexpr int kSplitHistCopies = 8;
 
+// Tries of the selecting workgroup's wait for a staged entry (each a
+// device-scope load and a short sleep, about a microsecond): the entries it
+// waits for are stored by workgroups that counted in before it and store
+// them right after their select, so the bound is only a guard; an entry it
+// gives up on counts as no item, and its rank's output is -1.
+constexpr int kStageSpins = 1 << 16;
+
 // The split layout's final select over the staged lists at `lists` (list j
 // at j * kStageListLen: the best cnt_j = min(k, pages of chunk j) of chunk
-// j, descending, composites in the high half, row ids in the low half): the
-// k best of the workers lists, emit(rank, composite) for rank 0 .. k-1 (from
-// wave 0); each row id goes to rid_lds at its composite's segment position.
+// j, descending, composites in the high half, row ids in the low half; a
+// staged entry is never 0): the k best of the workers lists, emit(rank,
+// composite) for rank 0 .. k-1 (from wave 0, composite 0 for a rank without
+// an item); each row id goes to rid_lds at its composite's segment position.
+// kOwnKept: list `own` (this workgroup's) was not stored and is read from
+// own_lds, and the other lists may still be on their way (every list place
+// is 0 until its workgroup stores it): an entry that is still 0 is loaded
+// again.  Otherwise every list, this workgroup's too, has been stored and
+// its stores have completed.  Every entry read from the zone is cleared
+// after it is read, so the zone is all zero again when the launch ends.
 // Lane l of wave w holds the elements g = (w * 64 + l) * kR + u, element g
 // being place g % lk of list g / lk (lk = k rounded up to a power of two, so
 // the lists are sorted runs of lk elements), every other list reversed when
 // a wave holds several, so that the bitonic sort starts at runs of 2 * lk.
 // Every thread of the workgroup calls it (it holds barriers).
-template <int T, int kR, typename Emit>
-__device__ __forceinline__ void merge_staged(const uint64_t* lists, int workers, int k, int lk, long long n,
-                                             int chunk, int32_t* rid_lds, vtx::BitonicRunShared<T>& bs, Emit emit) {
+template <int T, int kR, bool kOwnKept, typename Emit>
+__device__ __forceinline__ void merge_staged(uint64_t* lists, int workers, int own, const uint64_t* own_lds, int k,
+                                             int lk, long long n, int chunk, int32_t* rid_lds,
+                                             vtx::BitonicRunShared<T>& bs, Emit emit) {
   const int lane = vtx::lane_id();
   const int wave = vtx::uniform(threadIdx.x / vtx::kWave);
   const bool alternate = vtx::kWave * kR >= 2 * lk;
   uint64_t e[kR];
-  bool ok[kR];
+  int at[kR];    // list * kStageListLen + place of an entry to read from the zone, else -1
+  int kept[kR];  // kOwnKept: place in own_lds of this workgroup's entry, else -1
 #pragma unroll
   for (int u = 0; u < kR; ++u) {  // every load issued before any is used (list 0, place 0 always exists)
     const int g = (wave * vtx::kWave + lane) * kR + u;
     const int list = g / lk, p = g % lk;
     const int place = (alternate && (list & 1)) ? lk - 1 - p : p;
-    ok[u] = list < workers && place < k && place < n - (long long)list * chunk;
-    e[u] = load_coherent(lists + (ok[u] ? (long long)list * kStageListLen + place : 0));
+    const bool ok = list < workers && place < k && place < n - (long long)list * chunk;
+    const bool mine = kOwnKept && list == own;
+    at[u] = ok && !mine ? list * kStageListLen + place : -1;
+    kept[u] = ok && mine ? place : -1;
+    e[u] = load_coherent(lists + (at[u] >= 0 ? at[u] : 0));
+  }
+  if constexpr (kOwnKept) {
+    // then the own list's entries, and the wait for entries not yet stored
+    // (the LDS reads come after every load has been issued, so that a read
+    // the compiler puts in a branch does not hold up the loads after it)
+#pragma unroll
+    for (int u = 0; u < kR; ++u) {
+      if (kept[u] >= 0) e[u] = own_lds[kept[u]];
+      else if (at[u] < 0) e[u] = 0;
+      else
+        for (int t = 0; e[u] == 0 && t < kStageSpins; ++t) {
+          __builtin_amdgcn_s_sleep(2);
+          e[u] = load_coherent(lists + at[u]);
+        }
+    }
   }
   uint32_t comp[kR];
 #pragma unroll
   for (int u = 0; u < kR; ++u) {
-    comp[u] = ok[u] ? (uint32_t)(e[u] >> 32) : 0u;
+    comp[u] = kOwnKept || at[u] >= 0 ? (uint32_t)(e[u] >> 32) : 0u;
     if (comp[u]) rid_lds[vtx::bitonic_position(comp[u])] = (int32_t)(uint32_t)e[u];
   }
+  // cleared after the row ids' LDS writes, which would otherwise wait for
+  // these stores
+#pragma unroll
+  for (int u = 0; u < kR; ++u)
+    if (at[u] >= 0) store_coherent(lists + at[u], (uint64_t)0);
   vtx::select_bitonic_run<T, kR>(comp, k, bs, emit, alternate ? lk : vtx::kWave * kR);
 }
 
@@ -691,10 +743,12 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   constexpr int kTailR = 8;  // scores per thread the selecting workgroup holds in registers
   constexpr bool cm_on = kCmRegs > 0;
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
+  constexpr bool kCountFirst = VPL > 2;  // staged lists: count in before the chunk's select (one workgroup per CU)
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T, kSplitHistCopies> sh;
   __shared__ vtx::BitonicRunShared<T> bsr;  // the selecting workgroup's bitonic select
   __shared__ int s_last;
+  __shared__ uint64_t own_list[kCountFirst ? kStageListLen : 1];  // the last one's own list (kCountFirst)
   __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
   __shared__ float qm_part[VPL * LPR][kMeanPartStride];                        // its second half's accumulators
   __shared__ __align__(16) uint16_t fresh_row[cm_on && VPL > 1 ? kWaves * kMaxQueryDim : 8];  // per wave, CMean
@@ -939,28 +993,89 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
     score_all();
   }
   // (wave 0 of chunk 0 always has pages, so the mean has been stored)
-  if (hier && c < workers) {  // uniform: this chunk's best k, staged as list c of the segment
+  // The staged lists' final merge by the selecting workgroup: `lists` are
+  // the segment's, `kept` whether this workgroup's own list is in own_list
+  // only (merge_staged).
+  auto merge_lists = [&](uint64_t* lists, auto kept_tag) {
+    constexpr bool kKept = decltype(kept_tag)::value;
+    // entries: workers lists of lk = k rounded up to a power of two places,
+    // kR per thread
+    const int lk = k <= 1 ? 1 : 1 << (32 - __builtin_clz((unsigned)(k - 1)));
+    const int total = workers * lk;
+    auto merge = [&](auto kr_tag) {
+      constexpr int kR = decltype(kr_tag)::value;
+      merge_staged<T, kR, kKept>(lists, workers, c, own_list, k, lk, n, kChunk, rid_lds, bsr,
+                                 [&](int rank, uint32_t cv) {
+                                   // (a rank without an item only after a wait given up on)
+                                   a.sidx[obase + rank] = !kKept || cv ? rid_lds[vtx::bitonic_position(cv)] : -1;
+                                 });
+    };
+    if (total <= T) {
+      merge(std::integral_constant<int, 1>{});
+    } else if constexpr (T >= 512) {  // (total <= kStageLists * kStageListLen = 2 * 512)
+      merge(std::integral_constant<int, 2>{});
+    } else {
+      if (total <= 2 * T) merge(std::integral_constant<int, 2>{});
+      else merge(std::integral_constant<int, 4>{});
+    }
+  };
+  // The selecting workgroup reads the staged lists by content: a staged
+  // entry is never 0, the zone is all zero between launches (the selecting
+  // workgroup clears every entry it reads), and an entry that is still 0 is
+  // loaded again, so no store has to have completed when a workgroup counts
+  // in.  With one workgroup per CU (wide rows, kCountFirst) the count-in
+  // goes out before the chunk's select, its round trip hidden by the select,
+  // and the last one keeps its own list in LDS only; the lists of the
+  // others, whose selects take as long, are in place or nearly when it reads
+  // them.  Where several workgroups share a CU their selects take uneven
+  // times, and the last to count in often found lists still being stored:
+  // there every workgroup stores its list, waits for the stores to complete
+  // and counts in on the arrival path below, so the last finds every list in
+  // place.  A workgroup that waits only waits for entries of workgroups that
+  // counted in before it, each of which stores its list right after its
+  // select and waits for nobody: every wait ends.
+  uint64_t* const seg_lists = hier ? a.stage + (long long)seg * kStageLists * kStageListLen : nullptr;
+  if (hier) {  // uniform (c < workers): this chunk's best k, handed over as list c of the segment
     const long long c0 = (long long)c * kChunk;
     if (hcomp) rid_lds[vtx::bitonic_position(hcomp) - c0] = hrid;
-    uint64_t* list = a.stage + ((long long)seg * kStageLists + c) * kStageListLen;
+    uint64_t* list = seg_lists + (long long)c * kStageListLen;
     uint32_t cv[1] = {hcomp};
-    vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {
-      if (cmp) store_coherent(list + rank, ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0]);
-    });
+    if constexpr (kCountFirst) {
+      int old = 0;
+      if (tid == 0) old = fetch_add_one_deferred(&counters[seg]);
+      vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {  // (wave 0)
+        const uint64_t e = ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0];
+        if (__builtin_amdgcn_readlane(old, 0) == workers - 1) own_list[rank] = e;
+        else if (cmp) store_coherent(list + rank, e);
+      });
+      if (tid == 0) {
+        const int last = old == workers - 1;
+        if (last) __hip_atomic_store(&counters[seg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (s_last) merge_lists(seg_lists, std::true_type{});
+      cm_tiles();
+      return;
+    } else {
+      vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {
+        if (cmp) store_coherent(list + rank, ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0]);
+      });
+    }
   }
 
   // ---- arrival: the last of the `workers` workgroups selects.  This is a
   // release/acquire handoff written out for its one kind of payload: the
-  // scores are device-scope atomic stores (written through to the point of
-  // coherence, never held dirty in an XCD's L2), and a release then only
-  // needs each wave to wait until its own stores have completed
-  // (s_waitcnt 0), which happens before the barrier after which one thread
-  // counts the workgroup in with a device-scope atomic.  The last workgroup
-  // reads the scores with device-scope atomic loads issued after that count.
-  // The compiler fences keep the compiler from moving memory operations
-  // across either side.  (A device-scope release fence or release RMW would
-  // also write back the XCD's whole L2 in every workgroup: measured 2.8 to
-  // 5.5 times the launch time at C3 and C5.)
+  // scores (or the staged lists) are device-scope atomic stores (written
+  // through to the point of coherence, never held dirty in an XCD's L2), and
+  // a release then only needs each wave to wait until its own stores have
+  // completed (s_waitcnt 0), which happens before the barrier after which
+  // one thread counts the workgroup in with a device-scope atomic.  The last
+  // workgroup reads them with device-scope atomic loads issued after that
+  // count.  The compiler fences keep the compiler from moving memory
+  // operations across either side.  (A device-scope release fence or release
+  // RMW would also write back the XCD's whole L2 in every workgroup:
+  // measured 2.8 to 5.5 times the launch time at C3 and C5.)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -979,26 +1094,12 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   // ---- top-k of the segment
-  if (hier) {  // uniform: merge the staged lists
-    // entries: workers lists of lk = k rounded up to a power of two places,
-    // kR per thread
-    const int lk = k <= 1 ? 1 : 1 << (32 - __builtin_clz((unsigned)(k - 1)));
-    const int total = workers * lk;
-    auto merge = [&](auto kr_tag) {
-      constexpr int kR = decltype(kr_tag)::value;
-      merge_staged<T, kR>(a.stage + (long long)seg * kStageLists * kStageListLen, workers, k, lk, n, kChunk, rid_lds,
-                          bsr, [&](int rank, uint32_t cv) { a.sidx[obase + rank] = rid_lds[vtx::bitonic_position(cv)]; });
-    };
-    if (total <= T) {
-      merge(std::integral_constant<int, 1>{});
-    } else if constexpr (T >= 512) {  // (total <= kStageLists * kStageListLen = 2 * 512)
-      merge(std::integral_constant<int, 2>{});
-    } else {
-      if (total <= 2 * T) merge(std::integral_constant<int, 2>{});
-      else merge(std::integral_constant<int, 4>{});
+  if constexpr (!kCountFirst) {
+    if (hier) {  // uniform: merge the staged lists
+      merge_lists(seg_lists, std::false_type{});
+      cm_tiles();
+      return;
     }
-    cm_tiles();
-    return;
   }
   // from the stored scores (device-coherent loads)
   const uint16_t* scs = a.score + start;
@@ -1474,11 +1575,11 @@ int fused_impl(const uint16_t* q, int64_t q_rows, int32_t group_size, const uint
 // for callers that cannot allocate.  Every device keeps its own copy of the
 // array until the process ends; the kernels take its device address
 // (queried once per device with that device current), never the host-side
-// name.  Each launch that completes leaves every counter it used at zero, so
-// the counters are cleared (by a fill kernel) on the first call on a device,
-// by vtx_indexer_fused_noalloc_reset, and again before the next call after a
-// launch this entry point could not issue.  Calls that overlap on one device
-// share the array and race.
+// name.  Each launch that completes leaves every counter it used, and every
+// staged list place, at zero, so the array is cleared (by a fill kernel) on
+// the first call on a device, by vtx_indexer_fused_noalloc_reset, and again
+// before the next call after a launch this entry point could not issue.
+// Calls that overlap on one device share the array and race.
 #include <mutex>
 
 namespace {
@@ -1495,12 +1596,13 @@ __global__ void clear_counters_kernel(int32_t* c, int64_t n) {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 int32_t* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
-bool g_scratch_dirty[kMaxDevices] = {};    // counters to clear before the next call
+bool g_scratch_dirty[kMaxDevices] = {};    // array to clear before the next call
 
-// Clears the counters on stream s; outside a graph capture it also waits for
-// the fill, so that a first call on another stream cannot run before it.
+// Clears the counters and the staging zone on stream s; outside a graph
+// capture it also waits for the fill, so that a first call on another stream
+// cannot run before it.
 int clear_counters(int32_t* p, hipStream_t s) {
-  clear_counters_kernel<<<64, 256, 0, s>>>(p, kStaticCounters);
+  clear_counters_kernel<<<256, 256, 0, s>>>(p, kStaticInts);
   int rc = vtx::check_launch("indexer_fused_noalloc (clearing the counters)");
   if (rc != VTX_OK) return rc;
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
