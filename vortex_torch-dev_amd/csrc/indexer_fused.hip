@@ -653,10 +653,10 @@ constexpr int kStageSpins = 1 << 16;
 // the lists are sorted runs of lk elements), every other list reversed when
 // a wave holds several, so that the bitonic sort starts at runs of 2 * lk.
 // Every thread of the workgroup calls it (it holds barriers).
-template <int T, int kR, bool kOwnKept, typename Emit>
+template <int T, int kR, bool kOwnKept, typename Bs32, typename Emit>
 __device__ __forceinline__ void merge_staged(uint64_t* lists, int workers, int own, const uint64_t* own_lds, int k,
                                              int lk, long long n, int chunk, int32_t* rid_lds,
-                                             vtx::BitonicRunShared<T>& bs, Emit emit) {
+                                             vtx::BitonicRunShared<T>& bs, Bs32& bs32, Emit emit) {
   const int lane = vtx::lane_id();
   const int wave = vtx::uniform(threadIdx.x / vtx::kWave);
   const bool alternate = vtx::kWave * kR >= 2 * lk;
@@ -700,7 +700,14 @@ __device__ __forceinline__ void merge_staged(uint64_t* lists, int workers, int o
 #pragma unroll
   for (int u = 0; u < kR; ++u)
     if (at[u] >= 0) store_coherent(lists + at[u], (uint64_t)0);
-  vtx::select_bitonic_run<T, kR>(comp, k, bs, emit, alternate ? lk : vtx::kWave * kR);
+  const int run = alternate ? lk : vtx::kWave * kR;
+  if constexpr (kOwnKept && kR == 1) {  // (lists of 32 where k <= 32: one register per lane in the merges)
+    if (k <= vtx::kMaxBitonicK) {
+      vtx::select_bitonic<T>(comp[0], k, bs32, emit, run);
+      return;
+    }
+  }
+  vtx::select_bitonic_run<T, kR>(comp, k, bs, emit, run);
 }
 
 // Split segments: a segment's middle pages are dealt, kChunk = kWaves * kPass
@@ -748,6 +755,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   __shared__ vtx::SelectShared<T, kSplitHistCopies> sh;
   __shared__ vtx::BitonicRunShared<T> bsr;  // the selecting workgroup's bitonic select
   __shared__ int s_last;
+  __shared__ vtx::BitonicShared<kCountFirst ? T : vtx::kWave> bs32;  // selects of k <= 32 (kCountFirst)
   __shared__ uint64_t own_list[kCountFirst ? kStageListLen : 1];  // the last one's own list (kCountFirst)
   __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
   __shared__ float qm_part[VPL * LPR][kMeanPartStride];                        // its second half's accumulators
@@ -1004,7 +1012,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
     const int total = workers * lk;
     auto merge = [&](auto kr_tag) {
       constexpr int kR = decltype(kr_tag)::value;
-      merge_staged<T, kR, kKept>(lists, workers, c, own_list, k, lk, n, kChunk, rid_lds, bsr,
+      merge_staged<T, kR, kKept>(lists, workers, c, own_list, k, lk, n, kChunk, rid_lds, bsr, bs32,
                                  [&](int rank, uint32_t cv) {
                                    // (a rank without an item only after a wait given up on)
                                    a.sidx[obase + rank] = !kKept || cv ? rid_lds[vtx::bitonic_position(cv)] : -1;
@@ -1043,11 +1051,13 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
     if constexpr (kCountFirst) {
       int old = 0;
       if (tid == 0) old = fetch_add_one_deferred(&counters[seg]);
-      vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {  // (wave 0)
+      auto hand = [&](int rank, uint32_t cmp) {  // (wave 0)
         const uint64_t e = ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0];
         if (__builtin_amdgcn_readlane(old, 0) == workers - 1) own_list[rank] = e;
         else if (cmp) store_coherent(list + rank, e);
-      });
+      };
+      if (k <= vtx::kMaxBitonicK) vtx::select_bitonic<T>(hcomp, k, bs32, hand);  // (lists of 32)
+      else vtx::select_bitonic_run<T, 1>(cv, k, bsr, hand);
       if (tid == 0) {
         const int last = old == workers - 1;
         if (last) __hip_atomic_store(&counters[seg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

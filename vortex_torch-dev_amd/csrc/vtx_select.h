@@ -514,6 +514,10 @@ __device__ __forceinline__ uint32_t wave_merge_desc(uint32_t v) {
   return v;
 }
 
+// The wave's 64 * kR values sorted descending (defined below).
+template <int kR>
+__device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR], int sorted_run = 1);
+
 // LDS of select_bitonic: two buffers of 32 composites per wave.
 template <int T>
 struct BitonicShared {
@@ -523,12 +527,22 @@ struct BitonicShared {
 // The k (<= 32) best composites of the workgroup, emit(rank, comp) for rank
 // 0 .. k-1 (called by lanes 0 .. k-1 of wave 0).  Every thread of the
 // workgroup calls it with its item (0: none); it contains barriers.
+// sorted_run: as for wave_sort_desc_run (the items already form sorted runs
+// of that length, alternately descending and ascending).
 template <int T, typename Emit>
-__device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShared<T>& bs, Emit emit) {
+__device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShared<T>& bs, Emit emit,
+                                               int sorted_run = 1) {
   constexpr int kWaves = T / kWave;
   const int lane = lane_id();
   const int wave = uniform(threadIdx.x / kWave);
-  uint32_t v = wave_sort_desc(comp);
+  uint32_t v = comp;
+  if (sorted_run > 1) {  // uniform
+    uint32_t r[1] = {comp};
+    wave_sort_desc_run<1>(r, sorted_run);
+    v = r[0];
+  } else {
+    v = wave_sort_desc(comp);
+  }
   if (lane < 32) bs.cand[0][wave * 32 + lane] = v;
   int buf = 0;
 #pragma unroll
@@ -571,7 +585,7 @@ __device__ __forceinline__ void bitonic_cx(uint32_t& lo, uint32_t& hi, bool keep
 // that length, run r descending for even r and ascending for odd r (what
 // the network's earlier stages leave), so those stages are skipped.
 template <int kR>
-__device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR], int sorted_run = 1) {
+__device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR], int sorted_run) {
   constexpr int N = kWave * kR;
   const int lane = lane_id();
 #pragma unroll
