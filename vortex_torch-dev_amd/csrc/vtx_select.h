@@ -563,8 +563,8 @@ __device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShar
 // selecting workgroup): lane l of a wave holds elements l * kR + u.  Each
 // wave sorts its 64 * kR composites descending (strides below kR inside a
 // lane, the others across lanes) and keeps its best 64; pairs of 64-lists are
-// merged with two elements per lane (element 2l + u; a list against a
-// reversed one is bitonic) until wave 0 holds the best 64 in order.
+// merged, one element per lane, keeping the best 64 of each pair, until wave
+// 0 holds the best 64 in order.
 constexpr int kMaxBitonicRunK = 64;
 
 template <int T>
@@ -610,57 +610,36 @@ __device__ __forceinline__ void wave_sort_desc_run(uint32_t (&v)[kR], int sorted
   }
 }
 
-// A bitonic sequence of 128 values (element 2 * lane + u) sorted descending.
-__device__ __forceinline__ void wave_merge_desc2(uint32_t (&v)[2]) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int j = 2 * kWave / 2; j > 1; j >>= 1) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const uint32_t o = xshfl_u32(v[u], j / 2);
-      v[u] = ((2 * lane + u) & j) == 0 ? (v[u] > o ? v[u] : o) : (v[u] < o ? v[u] : o);
-    }
-  }
-  bitonic_cx(v[0], v[1], true);
-}
-
 // The k (<= 64) best of the T / 64 lists of 64 composites in bs.cand[0]
 // (list w at w * 64, each sorted descending, 0 for no item), merged pairwise
-// with two elements per lane (element 2l + u; a list against a reversed one
-// is bitonic) until wave 0 holds the best 64 in order: emit(rank, comp) for
-// rank 0 .. k-1, from wave 0.  Every thread of the workgroup calls it; it
-// starts with a barrier (after which bs.cand[0] and whatever else the caller
-// wrote to LDS are visible) and holds one per merge round.
+// until wave 0 holds the best 64 in order: emit(rank, comp) for rank
+// 0 .. k-1, from lanes 0 .. k-1 of wave 0.  A pair's best 64 are, lane by
+// lane, the larger of list a's place l and list b's place 63 - l (the first
+// compare-exchange of the bitonic merge of a and reversed b; the smaller
+// halves are dropped), a bitonic sequence that 6 steps sort (one register
+// per lane).  Every thread of the workgroup calls it; it starts with a
+// barrier (after which bs.cand[0] and whatever else the caller wrote to LDS
+// are visible) and holds one per merge round.
 template <int T, typename Emit>
 __device__ __forceinline__ void merge_lists_bitonic_run(int k, BitonicRunShared<T>& bs, Emit emit) {
   constexpr int kWaves = T / kWave;
   static_assert(kWaves >= 2, "two or more lists");
   const int lane = lane_id();
   const int wave = uniform(threadIdx.x / kWave);
-  uint32_t v[2] = {0u, 0u};
+  uint32_t v = 0u;
   int buf = 0;
 #pragma unroll
   for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 64 become w / 2
     __syncthreads();
     if (wave < w / 2) {  // uniform
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int e = 2 * lane + u;
-        v[u] = e < 64 ? bs.cand[buf][(2 * wave) * 64 + e] : bs.cand[buf][(2 * wave + 1) * 64 + (127 - e)];
-      }
-      wave_merge_desc2(v);
-      if (w > 2 && lane < 32) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) bs.cand[buf ^ 1][wave * 64 + 2 * lane + u] = v[u];
-      }
+      const uint32_t a = bs.cand[buf][(2 * wave) * 64 + lane];
+      const uint32_t b = bs.cand[buf][(2 * wave + 1) * 64 + 63 - lane];
+      v = wave_merge_desc(a > b ? a : b);
+      if (w > 2) bs.cand[buf ^ 1][wave * 64 + lane] = v;
     }
     buf ^= 1;
   }
-  if (wave == 0) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      if (2 * lane + u < k) emit(2 * lane + u, v[u]);
-  }
+  if (wave == 0 && lane < k) emit(lane, v);
 }
 
 // The k (<= 64) best of the workgroup's composites, kR per thread (0: none):
