@@ -655,6 +655,24 @@ __device__ __forceinline__ void select_bitonic_run(uint32_t (&comp)[kR], int k, 
   constexpr int kWaves = T / kWave;
   const int lane = lane_id();
   const int wave = uniform(threadIdx.x / kWave);
+  if constexpr (kR == 2 && kWaves > 1) {
+    if (sorted_run >= 64) {  // uniform: two sorted runs of 64, the second ascending
+      // the wave's best 64: element e of the first run against element
+      // e + 64 (lane + 32, same register), then lane i takes the i-th and
+      // the bitonic sequence is sorted in 6 steps
+      uint32_t top[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t o = xshfl_u32(comp[u], 32);
+        top[u] = comp[u] > o ? comp[u] : o;
+      }
+      const uint32_t t0 = (uint32_t)__shfl((int)top[0], lane >> 1, kWave);
+      const uint32_t t1 = (uint32_t)__shfl((int)top[1], lane >> 1, kWave);
+      bs.cand[0][wave * 64 + lane] = wave_merge_desc((lane & 1) ? t1 : t0);
+      merge_lists_bitonic_run<T>(k, bs, emit);
+      return;
+    }
+  }
   wave_sort_desc_run<kR>(comp, sorted_run);
   if constexpr (kWaves == 1) {
 #pragma unroll
