@@ -642,57 +642,54 @@ constexpr int kStageSpins = 1 << 16;
 // staged entry is never 0): the k best of the workers lists, emit(rank,
 // composite) for rank 0 .. k-1 (from wave 0, composite 0 for a rank without
 // an item); each row id goes to rid_lds at its composite's segment position.
-// kOwnKept: list `own` (this workgroup's) was not stored and is read from
-// own_lds, and the other lists may still be on their way (every list place
-// is 0 until its workgroup stores it): an entry that is still 0 is loaded
-// again.  Otherwise every list, this workgroup's too, has been stored and
-// its stores have completed.  Every entry read from the zone is cleared
-// after it is read, so the zone is all zero again when the launch ends.
+// List `own` (this workgroup's) was not stored and is read from own_lds; the
+// other lists may still be on their way (every list place is 0 until its
+// workgroup stores it): an entry that is still 0 is loaded again.  Every
+// entry read from the zone is cleared after it is read, so the zone is all
+// zero again when the launch ends.
 // Lane l of wave w holds the elements g = (w * 64 + l) * kR + u, element g
 // being place g % lk of list g / lk (lk = k rounded up to a power of two, so
 // the lists are sorted runs of lk elements), every other list reversed when
 // a wave holds several, so that the bitonic sort starts at runs of 2 * lk.
 // Every thread of the workgroup calls it (it holds barriers).
-template <int T, int kR, bool kOwnKept, typename Bs32, typename Emit>
+template <int T, int kR, typename Emit>
 __device__ __forceinline__ void merge_staged(uint64_t* lists, int workers, int own, const uint64_t* own_lds, int k,
                                              int lk, long long n, int chunk, int32_t* rid_lds,
-                                             vtx::BitonicRunShared<T>& bs, Bs32& bs32, Emit emit) {
+                                             vtx::BitonicRunShared<T>& bs, vtx::BitonicShared<T>& bs32, Emit emit) {
   const int lane = vtx::lane_id();
   const int wave = vtx::uniform(threadIdx.x / vtx::kWave);
   const bool alternate = vtx::kWave * kR >= 2 * lk;
   uint64_t e[kR];
   int at[kR];    // list * kStageListLen + place of an entry to read from the zone, else -1
-  int kept[kR];  // kOwnKept: place in own_lds of this workgroup's entry, else -1
+  int kept[kR];  // place in own_lds of this workgroup's entry, else -1
 #pragma unroll
   for (int u = 0; u < kR; ++u) {  // every load issued before any is used (list 0, place 0 always exists)
     const int g = (wave * vtx::kWave + lane) * kR + u;
     const int list = g / lk, p = g % lk;
     const int place = (alternate && (list & 1)) ? lk - 1 - p : p;
     const bool ok = list < workers && place < k && place < n - (long long)list * chunk;
-    const bool mine = kOwnKept && list == own;
+    const bool mine = list == own;
     at[u] = ok && !mine ? list * kStageListLen + place : -1;
     kept[u] = ok && mine ? place : -1;
     e[u] = load_coherent(lists + (at[u] >= 0 ? at[u] : 0));
   }
-  if constexpr (kOwnKept) {
-    // then the own list's entries, and the wait for entries not yet stored
-    // (the LDS reads come after every load has been issued, so that a read
-    // the compiler puts in a branch does not hold up the loads after it)
+  // then the own list's entries, and the wait for entries not yet stored
+  // (the LDS reads come after every load has been issued, so that a read the
+  // compiler puts in a branch does not hold up the loads after it)
 #pragma unroll
-    for (int u = 0; u < kR; ++u) {
-      if (kept[u] >= 0) e[u] = own_lds[kept[u]];
-      else if (at[u] < 0) e[u] = 0;
-      else
-        for (int t = 0; e[u] == 0 && t < kStageSpins; ++t) {
-          __builtin_amdgcn_s_sleep(2);
-          e[u] = load_coherent(lists + at[u]);
-        }
-    }
+  for (int u = 0; u < kR; ++u) {
+    if (kept[u] >= 0) e[u] = own_lds[kept[u]];
+    else if (at[u] < 0) e[u] = 0;
+    else
+      for (int t = 0; e[u] == 0 && t < kStageSpins; ++t) {
+        __builtin_amdgcn_s_sleep(2);
+        e[u] = load_coherent(lists + at[u]);
+      }
   }
   uint32_t comp[kR];
 #pragma unroll
   for (int u = 0; u < kR; ++u) {
-    comp[u] = kOwnKept || at[u] >= 0 ? (uint32_t)(e[u] >> 32) : 0u;
+    comp[u] = (uint32_t)(e[u] >> 32);
     if (comp[u]) rid_lds[vtx::bitonic_position(comp[u])] = (int32_t)(uint32_t)e[u];
   }
   // cleared after the row ids' LDS writes, which would otherwise wait for
@@ -701,7 +698,7 @@ __device__ __forceinline__ void merge_staged(uint64_t* lists, int workers, int o
   for (int u = 0; u < kR; ++u)
     if (at[u] >= 0) store_coherent(lists + at[u], (uint64_t)0);
   const int run = alternate ? lk : vtx::kWave * kR;
-  if constexpr (kOwnKept && kR == 1) {  // (lists of 32 where k <= 32: one register per lane in the merges)
+  if constexpr (kR == 1) {  // (lists of 32 where k <= 32: one register per lane in the merges)
     if (k <= vtx::kMaxBitonicK) {
       vtx::select_bitonic<T>(comp[0], k, bs32, emit, run);
       return;
@@ -750,13 +747,12 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   constexpr int kTailR = 8;  // scores per thread the selecting workgroup holds in registers
   constexpr bool cm_on = kCmRegs > 0;
   constexpr int kLocRegs = kCmRegs > 0 ? kCmRegs : 1;
-  constexpr bool kCountFirst = VPL > 2;  // staged lists: count in before the chunk's select (one workgroup per CU)
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ vtx::SelectShared<T, kSplitHistCopies> sh;
   __shared__ vtx::BitonicRunShared<T> bsr;  // the selecting workgroup's bitonic select
   __shared__ int s_last;
-  __shared__ vtx::BitonicShared<kCountFirst ? T : vtx::kWave> bs32;  // selects of k <= 32 (kCountFirst)
-  __shared__ uint64_t own_list[kCountFirst ? kStageListLen : 1];  // the last one's own list (kCountFirst)
+  __shared__ vtx::BitonicShared<T> bs32;                 // staged selects of k <= 32 (lists of 32)
+  __shared__ uint64_t own_list[kStageListLen];             // staged: the selecting workgroup's own list
   __shared__ __align__(16) uint16_t qm_row[kMaxQueryDim];                      // query mean, G > kQRegs
   __shared__ float qm_part[VPL * LPR][kMeanPartStride];                        // its second half's accumulators
   __shared__ __align__(16) uint16_t fresh_row[cm_on && VPL > 1 ? kWaves * kMaxQueryDim : 8];  // per wave, CMean
@@ -1001,84 +997,71 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
     score_all();
   }
   // (wave 0 of chunk 0 always has pages, so the mean has been stored)
-  // The staged lists' final merge by the selecting workgroup: `lists` are
-  // the segment's, `kept` whether this workgroup's own list is in own_list
-  // only (merge_staged).
-  auto merge_lists = [&](uint64_t* lists, auto kept_tag) {
-    constexpr bool kKept = decltype(kept_tag)::value;
-    // entries: workers lists of lk = k rounded up to a power of two places,
-    // kR per thread
-    const int lk = k <= 1 ? 1 : 1 << (32 - __builtin_clz((unsigned)(k - 1)));
-    const int total = workers * lk;
-    auto merge = [&](auto kr_tag) {
-      constexpr int kR = decltype(kr_tag)::value;
-      merge_staged<T, kR, kKept>(lists, workers, c, own_list, k, lk, n, kChunk, rid_lds, bsr, bs32,
-                                 [&](int rank, uint32_t cv) {
-                                   // (a rank without an item only after a wait given up on)
-                                   a.sidx[obase + rank] = !kKept || cv ? rid_lds[vtx::bitonic_position(cv)] : -1;
-                                 });
-    };
-    if (total <= T) {
-      merge(std::integral_constant<int, 1>{});
-    } else if constexpr (T >= 512) {  // (total <= kStageLists * kStageListLen = 2 * 512)
-      merge(std::integral_constant<int, 2>{});
-    } else {
-      if (total <= 2 * T) merge(std::integral_constant<int, 2>{});
-      else merge(std::integral_constant<int, 4>{});
-    }
-  };
-  // The selecting workgroup reads the staged lists by content: a staged
+  // Staged segments: this chunk's best k, handed over as list c of the
+  // segment.  The selecting workgroup reads the lists by content: a staged
   // entry is never 0, the zone is all zero between launches (the selecting
   // workgroup clears every entry it reads), and an entry that is still 0 is
   // loaded again, so no store has to have completed when a workgroup counts
-  // in.  With one workgroup per CU (wide rows, kCountFirst) the count-in
-  // goes out before the chunk's select, its round trip hidden by the select,
-  // and the last one keeps its own list in LDS only; the lists of the
-  // others, whose selects take as long, are in place or nearly when it reads
-  // them.  Where several workgroups share a CU their selects take uneven
-  // times, and the last to count in often found lists still being stored:
-  // there every workgroup stores its list, waits for the stores to complete
-  // and counts in on the arrival path below, so the last finds every list in
-  // place.  A workgroup that waits only waits for entries of workgroups that
+  // in.  The count-in goes out before the chunk's select, its round trip
+  // hidden by the select; the last one to count in keeps its own list in
+  // LDS only and merges.  It only waits for entries of workgroups that
   // counted in before it, each of which stores its list right after its
   // select and waits for nobody: every wait ends.
-  uint64_t* const seg_lists = hier ? a.stage + (long long)seg * kStageLists * kStageListLen : nullptr;
-  if (hier) {  // uniform (c < workers): this chunk's best k, handed over as list c of the segment
+  if (hier) {  // uniform (c < workers)
     const long long c0 = (long long)c * kChunk;
     if (hcomp) rid_lds[vtx::bitonic_position(hcomp) - c0] = hrid;
-    uint64_t* list = seg_lists + (long long)c * kStageListLen;
-    uint32_t cv[1] = {hcomp};
-    if constexpr (kCountFirst) {
-      int old = 0;
-      if (tid == 0) old = fetch_add_one_deferred(&counters[seg]);
-      auto hand = [&](int rank, uint32_t cmp) {  // (wave 0)
-        const uint64_t e = ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0];
-        if (__builtin_amdgcn_readlane(old, 0) == workers - 1) own_list[rank] = e;
-        else if (cmp) store_coherent(list + rank, e);
-      };
-      if (k <= vtx::kMaxBitonicK) vtx::select_bitonic<T>(hcomp, k, bs32, hand);  // (lists of 32)
-      else vtx::select_bitonic_run<T, 1>(cv, k, bsr, hand);
-      if (tid == 0) {
-        const int last = old == workers - 1;
-        if (last) __hip_atomic_store(&counters[seg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = last;
-      }
-      __syncthreads();
-      if (s_last) merge_lists(seg_lists, std::true_type{});
-      cm_tiles();
-      return;
+    uint64_t* lists = a.stage + (long long)seg * kStageLists * kStageListLen;
+    uint64_t* list = lists + (long long)c * kStageListLen;
+    int old = 0;
+    if (tid == 0) old = fetch_add_one_deferred(&counters[seg]);
+    auto hand = [&](int rank, uint32_t cmp) {  // (wave 0)
+      const uint64_t e = ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0];
+      if (__builtin_amdgcn_readlane(old, 0) == workers - 1) own_list[rank] = e;
+      else if (cmp) store_coherent(list + rank, e);
+    };
+    if (k <= vtx::kMaxBitonicK) {
+      vtx::select_bitonic<T>(hcomp, k, bs32, hand);  // (lists of 32)
     } else {
-      vtx::select_bitonic_run<T, 1>(cv, k, bsr, [&](int rank, uint32_t cmp) {
-        if (cmp) store_coherent(list + rank, ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0]);
-      });
+      uint32_t cv[1] = {hcomp};
+      vtx::select_bitonic_run<T, 1>(cv, k, bsr, hand);
     }
+    if (tid == 0) {
+      const int last = old == workers - 1;
+      if (last) __hip_atomic_store(&counters[seg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last) {
+      // entries: workers lists of lk = k rounded up to a power of two
+      // places, kR per thread
+      const int lk = k <= 1 ? 1 : 1 << (32 - __builtin_clz((unsigned)(k - 1)));
+      const int total = workers * lk;
+      auto merge = [&](auto kr_tag) {
+        constexpr int kR = decltype(kr_tag)::value;
+        merge_staged<T, kR>(lists, workers, c, own_list, k, lk, n, kChunk, rid_lds, bsr, bs32,
+                            [&](int rank, uint32_t cv) {
+                              // (a rank without an item only after a wait given up on)
+                              a.sidx[obase + rank] = cv ? rid_lds[vtx::bitonic_position(cv)] : -1;
+                            });
+      };
+      if (total <= T) {
+        merge(std::integral_constant<int, 1>{});
+      } else if constexpr (T >= 512) {  // (total <= kStageLists * kStageListLen = 2 * 512)
+        merge(std::integral_constant<int, 2>{});
+      } else {
+        if (total <= 2 * T) merge(std::integral_constant<int, 2>{});
+        else merge(std::integral_constant<int, 4>{});
+      }
+    }
+    cm_tiles();
+    return;
   }
 
-  // ---- arrival: the last of the `workers` workgroups selects.  This is a
-  // release/acquire handoff written out for its one kind of payload: the
-  // scores (or the staged lists) are device-scope atomic stores (written
-  // through to the point of coherence, never held dirty in an XCD's L2), and
-  // a release then only needs each wave to wait until its own stores have
+  // ---- arrival (unstaged segments): the last of the `workers` workgroups
+  // selects.  This is a release/acquire handoff written out for its one kind
+  // of payload: the scores are device-scope atomic stores (written through
+  // to the point of coherence, never held dirty in an XCD's L2), and a
+  // release then only needs each wave to wait until its own stores have
   // completed (s_waitcnt 0), which happens before the barrier after which
   // one thread counts the workgroup in with a device-scope atomic.  The last
   // workgroup reads them with device-scope atomic loads issued after that
@@ -1103,15 +1086,7 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
   }
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
-  // ---- top-k of the segment
-  if constexpr (!kCountFirst) {
-    if (hier) {  // uniform: merge the staged lists
-      merge_lists(seg_lists, std::false_type{});
-      cm_tiles();
-      return;
-    }
-  }
-  // from the stored scores (device-coherent loads)
+  // ---- top-k of the segment, from the stored scores (device-coherent loads)
   const uint16_t* scs = a.score + start;
   if (tail_bitonic) {  // uniform
     // thread t holds positions u * T + t (each load coalesced across the
