@@ -1014,8 +1014,8 @@ __global__ __launch_bounds__(T, (VPL == 1 ? 4 : 1)) void indexer_split_kernel(co
     uint64_t* list = lists + (long long)c * kStageListLen;
     int old = 0;
     if (tid == 0) old = fetch_add_one_deferred(&counters[seg]);
-    auto hand = [&](int rank, uint32_t cmp) {  // (wave 0)
-      const uint64_t e = ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0];
+    auto hand = [&](int rank, uint32_t cmp) {  // (wave 0; cmp 0: a rank past the chunk's pages)
+      const uint64_t e = cmp ? ((uint64_t)cmp << 32) | (uint32_t)rid_lds[vtx::bitonic_position(cmp) - c0] : 0;
       if (__builtin_amdgcn_readlane(old, 0) == workers - 1) own_list[rank] = e;
       else if (cmp) store_coherent(list + rank, e);
     };
