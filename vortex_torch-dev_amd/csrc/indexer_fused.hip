@@ -709,11 +709,14 @@ __device__ __forceinline__ void merge_staged(uint64_t* lists, int workers, int o
 
 // Split segments: a segment's middle pages are dealt, kChunk = kWaves * kPass
 // at a time, to `cps` workgroups (chunk c takes chunks c, c + cps, ...).  Each
-// workgroup scores its pages and stores the scores; the one that finishes
-// last (per-segment arrival counter in `counters`) selects the top-k from the
-// stored scores.  Nothing waits on another workgroup, so every workgroup runs
-// to completion whatever the others do.  The last one resets the counter to
-// zero for the next launch.
+// workgroup scores its pages and stores the scores; the one that counts in
+// last (per-segment arrival counter in `counters`) selects the top-k, from
+// the stored scores or, for a staged segment, from the chunks' pre-selected
+// lists.  No workgroup waits for one that has not counted in: an unstaged
+// segment's workgroups wait for nobody, and a staged segment's selecting
+// workgroup waits only for lists of workgroups that counted in before it
+// (running, and waiting for nobody), so every workgroup runs to completion.
+// The last one resets the counter to zero for the next launch.
 //
 // Work ids are laid out XCD by XCD (workgroup b runs on XCD b % 8), so the
 // chunks of one segment usually share an L2 and the selecting workgroup reads
