@@ -480,7 +480,9 @@ __device__ __forceinline__ void select_emit(const uint64_t* sel, int k, long lon
 // shuffles, no barrier, overlapping the other waves' loads), keeps its best
 // 32 in LDS, and the lists are merged pairwise (a 32-descending list against
 // a reversed one is bitonic: 6 steps) until wave 0 holds the best 32 in
-// order.  kMaxBitonicK is the largest k it serves.
+// order; with eight waves the first round merges four lists per wave, so
+// that two barrier rounds remain instead of three.  kMaxBitonicK is the
+// largest k it serves.
 constexpr int kMaxBitonicK = 32;
 
 __device__ __forceinline__ uint32_t bitonic_comp(bool have, uint32_t key, int pos) {
@@ -545,8 +547,31 @@ __device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShar
   }
   if (lane < 32) bs.cand[0][wave * 32 + lane] = v;
   int buf = 0;
+  int w0 = kWaves;
+  if constexpr (kWaves == 8) {
+    // eight lists of 32 become two: wave w < 2 takes lists 4w .. 4w + 3,
+    // each half-wave the best 32 of a pair (a list against the other
+    // reversed: a bitonic 32), the halves sorted in opposite directions
+    // (together bitonic), then merged
+    __syncthreads();
+    if (wave < 2) {  // uniform
+      const int h = lane >> 5, i = lane & 31;
+      const int base = (4 * wave + 2 * h) * 32;
+      const uint32_t x = bs.cand[0][base + i], y = bs.cand[0][base + 32 + 31 - i];
+      v = x > y ? x : y;
 #pragma unroll
-  for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 32 become w / 2
+      for (int j = 16; j > 0; j >>= 1) {
+        const uint32_t o = xshfl_u32(v, j);
+        v = (((lane & j) == 0) == (h == 0)) ? (v > o ? v : o) : (v < o ? v : o);
+      }
+      v = wave_merge_desc(v);
+      if (lane < 32) bs.cand[1][wave * 32 + lane] = v;
+    }
+    buf = 1;
+    w0 = 2;
+  }
+#pragma unroll
+  for (int w = w0; w > 1; w >>= 1) {  // w lists of 32 become w / 2
     __syncthreads();
     if (wave < w / 2) {  // uniform
       const int src = lane < 32 ? (2 * wave) * 32 + lane : (2 * wave + 1) * 32 + (kWave - 1 - lane);
