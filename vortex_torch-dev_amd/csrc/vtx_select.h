@@ -480,9 +480,9 @@ __device__ __forceinline__ void select_emit(const uint64_t* sel, int k, long lon
 // shuffles, no barrier, overlapping the other waves' loads), keeps its best
 // 32 in LDS, and the lists are merged pairwise (a 32-descending list against
 // a reversed one is bitonic: 6 steps) until wave 0 holds the best 32 in
-// order; with eight waves the first round merges four lists per wave, so
-// that two barrier rounds remain instead of three.  kMaxBitonicK is the
-// largest k it serves.
+// order; with eight (four) waves the first round merges four lists per
+// wave, so that two barrier rounds remain instead of three (one instead of
+// two).  kMaxBitonicK is the largest k it serves.
 constexpr int kMaxBitonicK = 32;
 
 __device__ __forceinline__ uint32_t bitonic_comp(bool have, uint32_t key, int pos) {
@@ -512,6 +512,17 @@ __device__ __forceinline__ uint32_t wave_merge_desc(uint32_t v) {
   for (int j = kWave / 2; j > 0; j >>= 1) {
     const uint32_t o = xshfl_u32(v, j);
     v = (i & j) == 0 ? (v > o ? v : o) : (v < o ? v : o);
+  }
+  return v;
+}
+
+// A bitonic sequence over the wave's 64 lanes sorted ascending.
+__device__ __forceinline__ uint32_t wave_merge_asc(uint32_t v) {
+  const int i = lane_id();
+#pragma unroll
+  for (int j = kWave / 2; j > 0; j >>= 1) {
+    const uint32_t o = xshfl_u32(v, j);
+    v = (i & j) == 0 ? (v < o ? v : o) : (v > o ? v : o);
   }
   return v;
 }
@@ -548,13 +559,13 @@ __device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShar
   if (lane < 32) bs.cand[0][wave * 32 + lane] = v;
   int buf = 0;
   int w0 = kWaves;
-  if constexpr (kWaves == 8) {
-    // eight lists of 32 become two: wave w < 2 takes lists 4w .. 4w + 3,
-    // each half-wave the best 32 of a pair (a list against the other
-    // reversed: a bitonic 32), the halves sorted in opposite directions
-    // (together bitonic), then merged
+  if constexpr (kWaves == 8 || kWaves == 4) {
+    // eight (four) lists of 32 become two (one): wave w < kWaves / 4 takes
+    // lists 4w .. 4w + 3, each half-wave the best 32 of a pair (a list
+    // against the other reversed: a bitonic 32), the halves sorted in
+    // opposite directions (together bitonic), then merged
     __syncthreads();
-    if (wave < 2) {  // uniform
+    if (wave < kWaves / 4) {  // uniform
       const int h = lane >> 5, i = lane & 31;
       const int base = (4 * wave + 2 * h) * 32;
       const uint32_t x = bs.cand[0][base + i], y = bs.cand[0][base + 32 + 31 - i];
@@ -565,10 +576,10 @@ __device__ __forceinline__ void select_bitonic(uint32_t comp, int k, BitonicShar
         v = (((lane & j) == 0) == (h == 0)) ? (v > o ? v : o) : (v < o ? v : o);
       }
       v = wave_merge_desc(v);
-      if (lane < 32) bs.cand[1][wave * 32 + lane] = v;
+      if (kWaves > 4 && lane < 32) bs.cand[1][wave * 32 + lane] = v;
     }
     buf = 1;
-    w0 = 2;
+    w0 = kWaves / 4;
   }
 #pragma unroll
   for (int w = w0; w > 1; w >>= 1) {  // w lists of 32 become w / 2
@@ -653,8 +664,26 @@ __device__ __forceinline__ void merge_lists_bitonic_run(int k, BitonicRunShared<
   const int wave = uniform(threadIdx.x / kWave);
   uint32_t v = 0u;
   int buf = 0;
+  int w0 = kWaves;
+  if constexpr (kWaves == 4 || kWaves == 8) {
+    // first round, four lists per wave (wave w < kWaves / 4 takes lists
+    // 4w .. 4w + 3): each pair to its best 64, one sorted descending and
+    // the other ascending (together bitonic), then the best 64 of both
+    __syncthreads();
+    if (wave < kWaves / 4) {  // uniform
+      const int b0 = 4 * wave * 64;
+      const uint32_t a = bs.cand[0][b0 + lane], b = bs.cand[0][b0 + 64 + 63 - lane];
+      const uint32_t c = bs.cand[0][b0 + 128 + lane], d = bs.cand[0][b0 + 192 + 63 - lane];
+      const uint32_t x = wave_merge_desc(a > b ? a : b);
+      const uint32_t y = wave_merge_asc(c > d ? c : d);
+      v = wave_merge_desc(x > y ? x : y);
+      if (kWaves > 4) bs.cand[1][wave * 64 + lane] = v;
+    }
+    buf = 1;
+    w0 = kWaves / 4;
+  }
 #pragma unroll
-  for (int w = kWaves; w > 1; w >>= 1) {  // w lists of 64 become w / 2
+  for (int w = w0; w > 1; w >>= 1) {  // w lists of 64 become w / 2
     __syncthreads();
     if (wave < w / 2) {  // uniform
       const uint32_t a = bs.cand[buf][(2 * wave) * 64 + lane];
